@@ -1,0 +1,311 @@
+#!/usr/bin/env python3
+"""Benchmark of the 4-bit quantized matmul path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
+
+Headline (BASELINE metric "4-bit GEMV achieved HBM GB/s at M=1"): one step is the
+9B-class decode layer's six projections (q, k, v, o, gate_up, down)
+at M=1, each one launch of the decode kernel, 4-bit affine g64 with fp16 scales, weights
+N(0, 0.02) quantized on the device and activations fp16 N(0, 1). Every step uses the next
+of >= 1 GiB of distinct weight copies so that the 256 MB Infinity Cache cannot serve
+re-reads. Steps are replayed from HIP graphs (one per copy) so that host launch cost does
+not pace the GPU. value = algorithmic bytes of the step / measured time per step.
+
+Also reported under "detail": the M=5 layer, the 27B layer at M=1 and M=8 (config 3), the
+27B prefill layer at M=2048 (config 4, TFLOP/s against the dense fp16 MFMA peak), each
+projection's kernel time, and the CPU baseline: the reference's numpy dequant + fp32
+matmul (oracle.linear_affine_cpu_f32) on a bounded sample, timed on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, 2.5 PFLOP/s
+CACHE_DEFEAT_BYTES = 1 << 30   # rotate >= 1 GiB of distinct weights
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_layer_copies(shapes, copies, seed, device, scale_dtype):
+    from raceline_amd import synth
+
+    layers = []
+    for c in range(copies):
+        layers.append([synth.random_affine(N, K, seed + 1000 * c + i, device, scale_dtype=scale_dtype)
+                       for i, (_, K, N) in enumerate(shapes)])
+    return layers
+
+
+def layer_bytes(shapes, M):
+    from raceline_amd.configs import linear_bytes
+
+    return sum(linear_bytes(M, K, N) for _, K, N in shapes)
+
+
+def copies_for(shapes):
+    per = layer_bytes(shapes, 1)
+    return max(2, -(-CACHE_DEFEAT_BYTES // per))
+
+
+class LayerRunner:
+    """Pre-built buffers and HIP graphs of the layer's projections: one graph per weight
+    copy (a single step) and one holding a step on every copy in turn. Graphs are
+    captured and replayed on one stream, which the timing events bracket."""
+
+    def __init__(self, layers, shapes, M, device, kernel=0, outliers=0.0):
+        import torch
+
+        from raceline_amd import ops, synth
+
+        self.torch = torch
+        self.layers, self.shapes, self.M = layers, shapes, M
+        self.xs = {K: synth.random_activations(M, K, 7 + K, device, outliers) for _, K, _ in shapes}
+        self.ys = [torch.empty((M, N), dtype=torch.float32, device=device) for _, _, N in shapes]
+        self.kernel = kernel
+        # grow the workspace to its largest size before capture (no allocation inside a graph)
+        for (_, K, N) in shapes:
+            ops._WS.get(device, ops.workspace_bytes(M, K, N))
+        self.stream = torch.cuda.Stream()
+        with torch.cuda.stream(self.stream):
+            for c in range(len(layers)):
+                self.run_eager(c)          # every call is valid before it is captured
+        torch.cuda.synchronize()
+        self.step_graphs = []
+        for c in range(len(layers)):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.stream):
+                self.run_eager(c)
+            self.step_graphs.append(g)
+        self.round_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.round_graph, stream=self.stream):
+            for c in range(len(layers)):
+                self.run_eager(c)
+        torch.cuda.synchronize()
+
+    def run_eager(self, c, only=None):
+        from raceline_amd import ops
+
+        for i, ((_, K, N), wt) in enumerate(zip(self.shapes, self.layers[c])):
+            if only is not None and i != only:
+                continue
+            ops.linear(self.xs[K], wt, out=self.ys[i], kernel=self.kernel)
+
+    def run_steps(self, first, count):
+        """Replays `count` steps starting at copy `first`: whole rounds from the round graph."""
+        n = len(self.step_graphs)
+        i = 0
+        while i < count:
+            if (first + i) % n == 0 and count - i >= n:
+                self.round_graph.replay()
+                i += n
+            else:
+                self.step_graphs[(first + i) % n].replay()
+                i += 1
+
+
+def time_steps(runner, steps, warmup):
+    torch = runner.torch
+    with torch.cuda.stream(runner.stream):
+        runner.run_steps(0, warmup)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        first = -(-warmup // len(runner.step_graphs)) * len(runner.step_graphs)  # start on a round boundary
+        start.record()
+        runner.run_steps(first, steps)
+        end.record()
+        torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps      # seconds per step
+
+
+def time_kernel(layers, shapes, M, idx, device, launches, kernel=0, outliers=0.0):
+    """Average duration of projection idx's kernel: a captured graph of `launches`
+    back-to-back launches over the rotating copies, replayed between two events on the
+    stream the kernels run on."""
+    import torch
+
+    from raceline_amd import ops, synth
+
+    _, K, N = shapes[idx]
+    x = synth.random_activations(M, K, 99, device, outliers)
+    y = torch.empty((M, N), dtype=torch.float32, device=device)
+    ops._WS.get(device, ops.workspace_bytes(M, K, N))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for c in range(len(layers)):
+            ops.linear(x, layers[c][idx], out=y, kernel=kernel)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(launches):
+            ops.linear(x, layers[i % len(layers)][idx], out=y, kernel=kernel)
+    with torch.cuda.stream(stream):
+        g.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        g.replay()
+        end.record()
+        torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / launches
+
+
+def cpu_baseline(device, budget_s=15.0):
+    """The reference's CPU path (numpy dequant + fp32 BLAS matmul, as restated in the
+    oracle) on the 9B layer at M=1, weights copied from the GPU inputs' generator."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+    from raceline_amd import synth
+    from raceline_amd.configs import CFG2_9B, linear_bytes
+
+    try:
+        from threadpoolctl import threadpool_info
+        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:  # noqa: BLE001
+        blas_threads = int(os.environ.get("OPENBLAS_NUM_THREADS", os.cpu_count() or 1))
+    mats = []
+    for i, (_, K, N) in enumerate(CFG2_9B):
+        wt = synth.random_affine(N, K, 4242 + i, device)
+        mats.append((K, N, wt.w.cpu().numpy().view(np.uint32), wt.s.cpu().view(torch.int16).numpy().view(np.uint16),
+                     wt.b.cpu().view(torch.int16).numpy().view(np.uint16)))
+    x = {K: synth.random_activations(1, K, 5, device).cpu().numpy() for _, K, _ in CFG2_9B}
+    total_bytes = 0
+    t_deq = t_mm = 0.0
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for K, N, w, s, b in mats:
+            a = time.perf_counter()
+            q = O.unpack_nibbles_u32(w)
+            W = O.dequant_affine(q, s, b, "f16")
+            m = time.perf_counter()
+            _ = x[K].astype(np.float32) @ W.T
+            e = time.perf_counter()
+            t_deq += m - a
+            t_mm += e - m
+            total_bytes += linear_bytes(1, K, N)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s or reps >= 5:
+            break
+    elapsed = t_deq + t_mm
+    return {
+        "value": total_bytes / elapsed / 1e9, "unit": "GB/s", "cores": int(blas_threads), "kind": "port",
+        "sample": f"9B decode layer (6 projections) at M=1, {reps} passes: numpy unpack+dequant "
+                  f"(1 thread) {t_deq / reps * 1e3:.1f} ms + fp32 BLAS matmul ({blas_threads} threads) "
+                  f"{t_mm / reps * 1e3:.1f} ms per layer; host has {os.cpu_count()} logical CPUs",
+        "ms_per_layer": elapsed / reps * 1e3,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--quick", action="store_true", help="headline only (no detail configs, no CPU baseline)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build's path runs on a single MI355X (the multi-GPU "
+              "sharding is a design only); run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from raceline_amd import lib
+    from raceline_amd.configs import CFG2_9B, CFG3_27B, CFG4_PREFILL_M, linear_bytes, linear_flops
+
+    lib.load()
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    dev = torch.device("cuda:0")
+    sd = torch.float16
+
+    # ---------------- headline: 9B decode layer, M = 1
+    copies = copies_for(CFG2_9B)
+    log(f"[bench] building {copies} copies of the 9B layer ({layer_bytes(CFG2_9B, 1) / 1e6:.1f} MB each)")
+    l9 = build_layer_copies(CFG2_9B, copies, 1, dev, sd)
+    run1 = LayerRunner(l9, CFG2_9B, 1, dev)
+    t1 = time_steps(run1, args.steps, args.warmup)
+    bytes1 = layer_bytes(CFG2_9B, 1)
+    value = bytes1 / t1 / 1e9
+    log(f"[bench] 9B layer M=1: {t1 * 1e6:.1f} us/step, {value:.0f} GB/s")
+
+    # dominant kernel: gate_up GEMV at M=1
+    gu = [i for i, (n, _, _) in enumerate(CFG2_9B) if n == "gate_up"][0]
+    _, Kg, Ng = CFG2_9B[gu]
+    t_gu = time_kernel(l9, CFG2_9B, 1, gu, dev, launches=4 * copies)
+    ach = linear_bytes(1, Kg, Ng) / t_gu / 1e9
+    roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "gemv_q4a_kernel<1,0,false> (9B gate_up, M=1, K=4096, N=24576)",
+                "avg_launch_us": round(t_gu * 1e6, 2), "algorithmic_bytes": linear_bytes(1, Kg, Ng)}
+
+    detail = {"layer_9b_m1": {"us_per_step": round(t1 * 1e6, 2), "GB/s": round(value, 1)}}
+    if not args.quick:
+        per = {}
+        for i, (name, K, N) in enumerate(CFG2_9B):
+            t = time_kernel(l9, CFG2_9B, 1, i, dev, launches=2 * copies)
+            per[name] = {"us": round(t * 1e6, 2), "GB/s": round(linear_bytes(1, K, N) / t / 1e9, 1)}
+        detail["proj_9b_m1"] = per
+        run5 = LayerRunner(l9, CFG2_9B, 5, dev)
+        t5 = time_steps(run5, args.steps, args.warmup)
+        detail["layer_9b_m5"] = {"us_per_step": round(t5 * 1e6, 2),
+                                 "GB/s": round(layer_bytes(CFG2_9B, 5) / t5 / 1e9, 1)}
+        del run1, run5, l9
+        torch.cuda.empty_cache()
+
+        c27 = copies_for(CFG3_27B)
+        log(f"[bench] building {c27} copies of the 27B layer")
+        l27 = build_layer_copies(CFG3_27B, c27, 2, dev, sd)
+        for M in (1, 8):
+            r = LayerRunner(l27, CFG3_27B, M, dev)
+            t = time_steps(r, args.steps, args.warmup)
+            detail[f"layer_27b_m{M}"] = {"us_per_step": round(t * 1e6, 2),
+                                         "GB/s": round(layer_bytes(CFG3_27B, M) / t / 1e9, 1)}
+            del r
+        # prefill: M = 2048, compute bound; two copies are plenty
+        rp = LayerRunner(l27[:2], CFG3_27B, CFG4_PREFILL_M, dev, outliers=0.01)
+        tp = time_steps(rp, max(4, args.steps // 5), 2)
+        flops = sum(linear_flops(CFG4_PREFILL_M, K, N) for _, K, N in CFG3_27B)
+        detail["prefill_27b_m2048"] = {"us_per_step": round(tp * 1e6, 1), "TFLOP/s": round(flops / tp / 1e12, 1),
+                                       "frac_of_mfma_peak": round(flops / tp / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+        log(f"[bench] 27B prefill: {flops / tp / 1e12:.1f} TFLOP/s")
+        del rp, l27
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.quick and not args.no_cpu:
+        log("[bench] CPU baseline (numpy dequant + BLAS matmul)")
+        cpu = cpu_baseline(dev)
+
+    line = {
+        "metric": "4-bit GEMV achieved HBM GB/s at M=1 (9B decode layer, 6 projections)",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(t1 * 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic (seeded N(0,0.02) weights quantized on device, fp16 N(0,1) activations)",
+        "config": {"workload": "9B-class decode layer projections q,k,v,o,gate_up,down; 4-bit affine g64, "
+                               "fp16 scales+biases, M=1, fp32 accumulate", "global_batch": 1, "seq_len": 1,
+                   "parallelism": "single GPU", "weight_copies": copies, "bytes_per_step": bytes1},
+        "roofline": roofline,
+        "cpu_baseline": None if cpu is None else {k: v for k, v in cpu.items() if k != "ms_per_layer"},
+        "detail": detail,
+    }
+    if cpu is not None:
+        line["cpu_baseline"]["value"] = round(cpu["value"], 3)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,60 @@
+// Library-level entry points: error mode, last error, device selection, workspace clearing.
+#include "rlq_common.h"
+#include "../../include/rlq.h"
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+namespace rlq {
+
+namespace {
+thread_local int t_fatal = 1;
+thread_local char t_error[512] = "";
+}  // namespace
+
+int fail(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(t_error, sizeof t_error, fmt, ap);
+  va_end(ap);
+  if (t_fatal) {
+    fprintf(stderr, "raceline: fatal: %s\n", t_error);
+    fflush(stderr);
+    exit(1);
+  }
+  return -1;
+}
+
+int check_hip(hipError_t e, const char *what) {
+  if (e == hipSuccess) return 0;
+  return fail("%s: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace rlq
+
+extern "C" {
+
+int rlq_abi_version(void) { return 1; }
+
+int rlq_set_fatal(int on) {
+  int old = rlq::t_fatal;
+  rlq::t_fatal = on ? 1 : 0;
+  return old;
+}
+
+const char *rlq_last_error(void) { return rlq::t_error; }
+
+int rlq_set_device(int device) {
+  RLQ_HIP(hipSetDevice(device));
+  return 0;
+}
+
+int rlq_workspace_clear(void *workspace, size_t bytes, void *stream) {
+  if (bytes == 0) return 0;
+  RLQ_REQUIRE(workspace != nullptr, "rlq_workspace_clear: null workspace of %zu bytes", bytes);
+  RLQ_HIP(hipMemsetAsync(workspace, 0, bytes, static_cast<hipStream_t>(stream)));
+  return 0;
+}
+
+}  // extern "C"

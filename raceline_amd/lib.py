@@ -1,0 +1,71 @@
+"""ctypes binding of libraceline_amd.so (the C ABI of include/rlq.h).
+
+Discovery follows raceline/engine.py:67-81 of the reference: the library named by
+RACELINE_LIB if set, else the one built next to this package. There is no fallback:
+without the built library every call raises, so nothing silently runs on the CPU.
+The binding puts the library in non-fatal mode and turns a failed call into a
+RuntimeError carrying the library's message.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_NAME = "libraceline_amd.so"
+
+c_int, c_size_t, c_void_p, c_char_p = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_char_p
+
+# name -> (restype, argtypes); the whole exported surface of include/rlq.h
+SIGNATURES = {
+    "rlq_abi_version": (c_int, []),
+    "rlq_set_fatal": (c_int, [c_int]),
+    "rlq_last_error": (c_char_p, []),
+    "rlq_set_device": (c_int, [c_int]),
+    "rlq_linear_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "rlq_workspace_clear": (c_int, [c_void_p, c_size_t, c_void_p]),
+    "rlq_linear_affine": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
+                                  c_void_p, c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "rlq_linear_affine_kernel": (c_int, [c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
+                                         c_int, c_void_p, c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "rlq_group_sums": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "rlq_dequant_affine": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "rlq_repack_blocked": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                   c_void_p, c_void_p]),
+}
+
+
+def library_path() -> str:
+    env = os.environ.get("RACELINE_LIB")
+    for path in (env, os.path.join(HERE, LIB_NAME)):
+        if path and os.path.isfile(path):
+            return path
+    raise RuntimeError(f"{LIB_NAME} not found: build it with `python -m raceline_amd.build` "
+                       "(or __graft_entry__.build()) or point RACELINE_LIB at it")
+
+
+@functools.lru_cache(maxsize=1)
+def load() -> ctypes.CDLL:
+    lib = ctypes.CDLL(library_path())
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+class RlqError(RuntimeError):
+    pass
+
+
+def call(name: str, *args):
+    """Calls rlq_<name> in non-fatal mode and raises RlqError on a nonzero status."""
+    lib = load()
+    lib.rlq_set_fatal(0)
+    rc = getattr(lib, name)(*args)
+    if isinstance(rc, int) and rc != 0 and SIGNATURES[name][0] is c_int and name not in (
+            "rlq_abi_version", "rlq_set_fatal"):
+        raise RlqError(f"{name}: {lib.rlq_last_error().decode(errors='replace')}")
+    return rc

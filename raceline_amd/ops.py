@@ -1,0 +1,154 @@
+"""Torch-facing host layer over the C ABI: the quantized linear of raceline's engine.
+
+Mirrors what Engine::encode_linear does for one QTensor (src/engine.mm:832-906): pick
+the kernel for the row count, bind the activations, the weight's codes, scales and
+biases and the output, and run it with ACCUM for the residual writers. Tensors are
+torch CUDA tensors (HBM plumbing only); every computation runs in libraceline_amd.so.
+"""
+
+from __future__ import annotations
+
+import threading
+from dataclasses import dataclass
+
+import torch
+
+from . import lib
+
+GROUP = 64
+F16, BF16 = 0, 1
+KERNEL_AUTO, KERNEL_GEMV, KERNEL_GEMM = 0, 1, 2
+
+
+def _ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def scale_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return F16
+    if dtype == torch.bfloat16:
+        return BF16
+    raise ValueError(f"scales must be float16 or bfloat16, not {dtype}")
+
+
+@dataclass
+class AffineWeight:
+    """A 4-bit affine matrix in the MLX layout (tools/convert.py:82-89): codes int32
+    [N][K/8] (bit pattern of the uint32 words), scales and biases [N][K/64] in float16
+    or bfloat16. Like the reference's QTensor (src/model_file.h:44-55) it may carry
+    named parts of a row-stacked matrix."""
+    w: torch.Tensor
+    s: torch.Tensor
+    b: torch.Tensor
+    parts: dict | None = None
+
+    def __post_init__(self):
+        if self.w.dtype not in (torch.int32, torch.uint32):
+            raise TypeError("codes must be 32-bit words")
+        N, K8 = self.w.shape
+        if self.s.shape != (N, K8 * 8 // GROUP) or self.b.shape != self.s.shape:
+            raise ValueError(f"scales/biases {tuple(self.s.shape)} do not match codes {tuple(self.w.shape)}")
+        if self.s.dtype != self.b.dtype:
+            raise TypeError("scales and biases must share a dtype")
+        for t in (self.w, self.s, self.b):
+            if not t.is_contiguous():
+                raise ValueError("weight tensors must be contiguous")
+
+    @property
+    def N(self) -> int:
+        return self.w.shape[0]
+
+    @property
+    def K(self) -> int:
+        return self.w.shape[1] * 8
+
+    @property
+    def scale_dtype(self) -> int:
+        return scale_code(self.s.dtype)
+
+    def part(self, name: str) -> "AffineWeight":
+        off, n = self.parts[name]
+        return AffineWeight(self.w[off:off + n], self.s[off:off + n], self.b[off:off + n])
+
+
+class _Workspaces:
+    """One zero-filled scratch buffer per device, grown on demand. Kernels leave it
+    zeroed, so it is cleared only when (re)allocated. Calls that use it must not
+    overlap on two streams of one device."""
+
+    def __init__(self):
+        self._bufs = {}
+        self._lock = threading.Lock()
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        key = device.index if device.index is not None else torch.cuda.current_device()
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+
+_WS = _Workspaces()
+
+
+def workspace_bytes(M: int, K: int, N: int) -> int:
+    return int(lib.load().rlq_linear_workspace_bytes(M, K, N))
+
+
+def linear(x: torch.Tensor, wt: AffineWeight, out: torch.Tensor | None = None, accum: bool = False,
+           kernel: int = KERNEL_AUTO, stream=None) -> torch.Tensor:
+    """out[m][n] (+)= sum_k x[m][k] * W[n][k] for fp16 x [M][>=K] (row stride x.stride(0))."""
+    if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be a row-major float16 matrix")
+    M, K, N = x.shape[0], wt.K, wt.N
+    if x.shape[1] < K:
+        raise ValueError(f"x has {x.shape[1]} columns, the weight needs {K}")
+    if out is None:
+        if accum:
+            raise ValueError("accum needs an output to add into")
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    if out.dtype != torch.float32 or out.stride(1) != 1 or out.shape[0] < M or out.shape[1] < N:
+        raise ValueError("out must be a row-major float32 [M][>=N] matrix")
+    nbytes = workspace_bytes(M, K, N)
+    ws = _WS.get(x.device, nbytes)
+    lib.call("rlq_linear_affine_kernel", kernel, _ptr(x), x.stride(0), M, K, N, _ptr(wt.w), _ptr(wt.s), _ptr(wt.b),
+             wt.scale_dtype, _ptr(out), out.stride(0), 1 if accum else 0, _ptr(ws), 0 if ws is None else ws.numel(),
+             _stream(stream))
+    return out
+
+
+def group_sums(x: torch.Tensor, K: int | None = None, stream=None) -> torch.Tensor:
+    K = x.shape[1] if K is None else K
+    out = torch.empty((x.shape[0], K // GROUP), dtype=torch.float32, device=x.device)
+    lib.call("rlq_group_sums", _ptr(x), x.stride(0), x.shape[0], K, _ptr(out), _stream(stream))
+    return out
+
+
+def dequant(wt: AffineWeight, stream=None) -> torch.Tensor:
+    out = torch.empty((wt.N, wt.K), dtype=torch.float32, device=wt.w.device)
+    lib.call("rlq_dequant_affine", _ptr(wt.w), _ptr(wt.s), _ptr(wt.b), wt.scale_dtype, wt.K, wt.N, _ptr(out),
+             _stream(stream))
+    return out
+
+
+def repack_blocked(w_blk: torch.Tensor, s_blk: torch.Tensor, b_blk: torch.Tensor, K: int, n_pad: int,
+                   row0: int, rows: int, scale_dtype: torch.dtype = torch.bfloat16, stream=None) -> AffineWeight:
+    """Blocked q4a tensor of a .rlm file (already in device memory) -> AffineWeight for
+    rows [row0, row0 + rows)."""
+    dev = w_blk.device
+    w = torch.empty((rows, K // 8), dtype=torch.int32, device=dev)
+    s = torch.empty((rows, K // GROUP), dtype=scale_dtype, device=dev)
+    b = torch.empty((rows, K // GROUP), dtype=scale_dtype, device=dev)
+    lib.call("rlq_repack_blocked", _ptr(w_blk), _ptr(s_blk), _ptr(b_blk), K, n_pad, row0, rows, _ptr(w), _ptr(s),
+             _ptr(b), _stream(stream))
+    return AffineWeight(w, s, b)

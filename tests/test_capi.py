@@ -1,0 +1,82 @@
+"""The C ABI library without a GPU: it loads, exports every function include/*.h declares,
+and rejects bad arguments the way the reference does (fatal "raceline: fatal: ..." and exit
+status 1 by default, src/metal_rt.mm:16-24), before any device work."""
+
+import glob
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+from raceline_amd import lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = []
+    for path in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        names += re.findall(r"\b(rlq_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_the_path():
+    names = declared_functions()
+    for must in ("rlq_linear_affine", "rlq_dequant_affine", "rlq_repack_blocked", "rlq_group_sums"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    L = lib.load()
+    missing = [n for n in declared_functions() if not hasattr(L, n)]
+    assert not missing, f"not exported: {missing}"
+    # the ctypes binding declares every one of them
+    assert set(declared_functions()) <= set(lib.SIGNATURES)
+    nm = subprocess.run(["nm", "-D", "--defined-only", lib.library_path()], capture_output=True, text=True)
+    if nm.returncode == 0:
+        exported = set(re.findall(r"\b(rlq_\w+)\b", nm.stdout))
+        assert set(declared_functions()) <= exported
+
+
+def test_abi_version_and_workspace_query():
+    L = lib.load()
+    assert L.rlq_abi_version() == 1
+    assert L.rlq_linear_workspace_bytes(1, 4096, 4096) > 0      # small N splits K over workgroups
+    assert L.rlq_linear_workspace_bytes(1, 100, 4096) == 0      # invalid K: nothing to size
+    # the split of K, hence the workspace per token row, does not depend on M
+    a = L.rlq_linear_workspace_bytes(1, 4096, 1024)
+    b = L.rlq_linear_workspace_bytes(8, 4096, 1024)
+    assert b > a
+
+
+def test_bad_arguments_return_an_error_in_nonfatal_mode():
+    with pytest.raises(lib.RlqError, match="multiple of the group size"):
+        lib.call("rlq_linear_affine", 16, 100, 1, 100, 10, 16, 16, 16, 0, 16, 10, 0, None, 0, None)
+    with pytest.raises(lib.RlqError, match="unknown scale dtype"):
+        lib.call("rlq_linear_affine", 16, 64, 1, 64, 10, 16, 16, 16, 7, 16, 10, 0, None, 0, None)
+    with pytest.raises(lib.RlqError, match="x_stride"):
+        lib.call("rlq_linear_affine", 16, 60, 1, 64, 10, 16, 16, 16, 0, 16, 10, 0, None, 0, None)
+    with pytest.raises(lib.RlqError, match="null pointer"):
+        lib.call("rlq_linear_affine", None, 64, 1, 64, 10, 16, 16, 16, 0, 16, 10, 0, None, 0, None)
+    with pytest.raises(lib.RlqError, match="block 256"):
+        lib.call("rlq_repack_blocked", 16, 16, 16, 64, 300, 0, 10, 16, 16, 16, None)
+    with pytest.raises(lib.RlqError, match="outside"):
+        lib.call("rlq_repack_blocked", 16, 16, 16, 64, 256, 200, 100, 16, 16, 16, None)
+    assert lib.load().rlq_last_error().decode().startswith("rlq_repack_blocked")
+
+
+def test_errors_are_fatal_by_default():
+    code = ("import ctypes, sys; sys.path.insert(0, %r); from raceline_amd import lib; "
+            "L = ctypes.CDLL(lib.library_path()); "
+            "L.rlq_linear_affine(ctypes.c_void_p(16), 100, 1, 100, 10, ctypes.c_void_p(16), ctypes.c_void_p(16), "
+            "ctypes.c_void_p(16), 0, ctypes.c_void_p(16), 10, 0, None, ctypes.c_size_t(0), None); "
+            "print('not reached')") % ROOT
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1
+    assert "raceline: fatal: rlq_linear_affine: K=100 is not a multiple of the group size 64" in r.stderr
+    assert "not reached" not in r.stdout

@@ -1,0 +1,166 @@
+"""Parity of the HIP affine 4-bit linear (decode GEMV and prefill GEMM) with the oracle.
+
+Bar: dequantized weights bit-exact; outputs max|y - ref| / rms(ref) <= 1e-3 against the
+fp64 dequant+matmul (oracle.linear_affine_f64), and the reference test's own criterion
+max|err| < 2e-3 * rms + 1e-4 (tests/test_linear.mm:178), both via oracle.check_close.
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.qdata import make_layer, make_x, sample_cols, to_dev, upload
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _run(gpu, x_np, wt, kernel=0, accum_into=None):
+    import torch
+
+    from raceline_amd import ops
+
+    x = to_dev(x_np, gpu)
+    out = None if accum_into is None else to_dev(accum_into.astype(np.float32), gpu)
+    y = ops.linear(x, wt, out=out, accum=accum_into is not None, kernel=kernel)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("sd", ["f16", "bf16"])
+def test_dequant_bit_exact(gpu, sd):
+    import torch
+
+    from raceline_amd import ops
+
+    rng = np.random.default_rng(100)
+    N, K = 300, 512
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    # scales over the whole finite range of the format, subnormals and both signs included
+    s = rng.integers(0, 1 << 16, size=(N, K // 64), dtype=np.uint32).astype(np.uint16)
+    b = rng.integers(0, 1 << 16, size=(N, K // 64), dtype=np.uint32).astype(np.uint16)
+    if sd == "f16":
+        s &= np.uint16(0x7BFF) | np.uint16(0x8000)     # keep exponents finite
+        b &= np.uint16(0x7BFF) | np.uint16(0x8000)
+    else:
+        s &= np.uint16(0x7F7F) | np.uint16(0x8000)
+        b &= np.uint16(0x7F7F) | np.uint16(0x8000)
+    wt = upload(q, s, b, sd, gpu)
+    got = ops.dequant(wt)
+    torch.cuda.synchronize()
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = O.dequant_affine(q, s, b, sd)
+    g = got.cpu().numpy()
+    same = (g.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(g) & np.isnan(ref))
+    assert same.all(), f"{(~same).sum()} dequantized weights differ"
+
+
+GEMV_CASES = [  # (M, K, N)
+    (1, 256, 32), (1, 4096, 4096), (5, 2560, 9216), (3, 9216, 2560), (2, 2560, 1000),
+    (8, 512, 2048), (16, 1024, 300), (32, 2048, 1024), (17, 640, 96), (1, 17408, 640), (4, 64, 33),
+]
+
+
+@pytest.mark.parametrize("M,K,N", GEMV_CASES)
+def test_gemv_parity(gpu, M, K, N):
+    sd = "f16" if (M + K + N) % 2 else "bf16"
+    q, s, b = make_layer(M * 1000 + N, N, K, sd)
+    x = make_x(K + M, M, K)
+    y = _run(gpu, x, upload(q, s, b, sd, gpu), kernel=1)
+    ref = O.linear_affine_f64(x, q, s, b, sd)
+    O.check_close(y[:, :N], ref, TOL, f"gemv M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (7, 4096, 1024), (32, 512, 96)])
+def test_gemv_accumulates(gpu, M, K, N):
+    q, s, b = make_layer(7, N, K)
+    x = make_x(8, M, K)
+    y0 = np.random.default_rng(9).standard_normal((M, N)).astype(np.float32)
+    y = _run(gpu, x, upload(q, s, b, "f16", gpu), kernel=1, accum_into=y0)
+    ref = O.linear_affine_f64(x, q, s, b) + y0.astype(np.float64)
+    O.check_close(y, ref, TOL, "gemv accum")
+
+
+GEMM_CASES = [(33, 256, 64), (130, 5120, 1024), (512, 2048, 1024), (70, 9216, 2560), (256, 1024, 300),
+              (40, 2560, 1000)]
+
+
+@pytest.mark.parametrize("M,K,N", GEMM_CASES)
+def test_gemm_parity(gpu, M, K, N):
+    sd = "f16" if (M + N) % 2 else "bf16"
+    q, s, b = make_layer(M * 7 + N, N, K, sd)
+    x = make_x(M + K, M, K, outliers=0.01)
+    y = _run(gpu, x, upload(q, s, b, sd, gpu), kernel=2)
+    ref = O.linear_affine_f64(x, q, s, b, sd)
+    O.check_close(y, ref, TOL, f"gemm M={M} K={K} N={N}")
+
+
+def test_gemm_accumulates(gpu):
+    M, K, N = 200, 1024, 384
+    q, s, b = make_layer(1, N, K)
+    x = make_x(2, M, K)
+    y0 = np.random.default_rng(3).standard_normal((M, N)).astype(np.float32)
+    y = _run(gpu, x, upload(q, s, b, "f16", gpu), kernel=2, accum_into=y0)
+    O.check_close(y, O.linear_affine_f64(x, q, s, b) + y0, TOL, "gemm accum")
+
+
+def test_rows_do_not_depend_on_other_rows(gpu):
+    """A token's result is bit-identical whatever rows share the call (the reference's
+    determinism rule, kernels/linear.metal:264-266): one row alone vs. inside M = 8."""
+    M, K, N = 8, 4096, 1024
+    q, s, b = make_layer(11, N, K)
+    x = make_x(12, M, K)
+    wt = upload(q, s, b, "f16", gpu)
+    y_all = _run(gpu, x, wt, kernel=1)
+    for m in (0, 3, 7):
+        y_one = _run(gpu, x[m:m + 1], wt, kernel=1)
+        np.testing.assert_array_equal(y_one[0], y_all[m])
+
+
+def test_repeat_calls_reuse_workspace(gpu):
+    """Split-K counters reset themselves: repeated calls give identical results."""
+    M, K, N = 1, 4096, 1024
+    q, s, b = make_layer(13, N, K)
+    x = make_x(14, M, K)
+    wt = upload(q, s, b, "f16", gpu)
+    first = _run(gpu, x, wt, kernel=1)
+    for _ in range(3):
+        np.testing.assert_array_equal(_run(gpu, x, wt, kernel=1), first)
+
+
+@pytest.mark.parametrize("sd", ["f16", "bf16"])
+def test_repack_blocked_round_trip(gpu, sd):
+    import torch
+
+    from raceline_amd import ops
+
+    K = 256
+    parts = [make_layer(20 + i, rows, K, sd) for i, rows in enumerate((200, 300))]
+    w, s, b, n_pad, offs = O.pack_blocked(parts)
+    wb, sb, bb = to_dev(w, gpu), to_dev(s.view(np.int16), gpu), to_dev(b.view(np.int16), gpu)
+    dt = torch.float16 if sd == "f16" else torch.bfloat16
+    for (off, rows), (q, s_p, b_p) in zip(offs, parts):
+        wt = ops.repack_blocked(wb, sb, bb, K, n_pad, off, rows, scale_dtype=dt)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(wt.w.cpu().numpy().view(np.uint32), O.pack_nibbles_u32(q))
+        np.testing.assert_array_equal(wt.s.cpu().view(torch.int16).numpy().view(np.uint16), s_p)
+        np.testing.assert_array_equal(wt.b.cpu().view(torch.int16).numpy().view(np.uint16), b_p)
+
+
+def test_group_sums(gpu):
+    import torch
+
+    from raceline_amd import ops
+
+    x = make_x(30, 5, 1024)
+    got = ops.group_sums(to_dev(x, gpu))
+    torch.cuda.synchronize()
+    # sequential fp32 sum, as kernels/linear.metal:42-44
+    ref = np.zeros((5, 16), np.float32)
+    for m in range(5):
+        for g in range(16):
+            acc = np.float32(0)
+            for v in x[m, 64 * g:64 * g + 64]:
+                acc = np.float32(acc + np.float32(v))
+            ref[m, g] = acc
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)

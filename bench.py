@@ -174,9 +174,9 @@ def cpu_baseline(device, budget_s=15.0):
         blas_threads = int(os.environ.get("OPENBLAS_NUM_THREADS", os.cpu_count() or 1))
     mats = []
     for i, (_, K, N) in enumerate(CFG2_9B):
-        wt = synth.random_affine(N, K, 4242 + i, device)
-        mats.append((K, N, wt.w.cpu().numpy().view(np.uint32), wt.s.cpu().view(torch.int16).numpy().view(np.uint16),
-                     wt.b.cpu().view(torch.int16).numpy().view(np.uint16)))
+        w, s, b = synth.random_affine(N, K, 4242 + i, device, packed=False)
+        mats.append((K, N, w.cpu().numpy().view(np.uint32), s.cpu().view(torch.int16).numpy().view(np.uint16),
+                     b.cpu().view(torch.int16).numpy().view(np.uint16)))
     x = {K: synth.random_activations(1, K, 5, device).cpu().numpy() for _, K, _ in CFG2_9B}
     total_bytes = 0
     t_deq = t_mm = 0.0
@@ -249,7 +249,7 @@ def main():
     ach = linear_bytes(1, Kg, Ng) / t_gu / 1e9
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "gemv_q4a_kernel<1,0,false> (9B gate_up, M=1, K=4096, N=24576)",
+                "kernel": "gemv_q4a_kernel<1,16,0,false> (9B gate_up, M=1, K=4096, N=24576)",
                 "avg_launch_us": round(t_gu * 1e6, 2), "algorithmic_bytes": linear_bytes(1, Kg, Ng)}
 
     detail = {"layer_9b_m1": {"us_per_step": round(t1 * 1e6, 2), "GB/s": round(value, 1)}}

@@ -44,46 +44,68 @@ const char *rlq_last_error(void);
 /* Selects the GPU for this thread's later calls (hipSetDevice). */
 int rlq_set_device(int device);
 
+/* ---------------------------------------------------------------- packed weights */
+
+/* The kernels read weights in a packed device layout made once at upload (the reference maps
+ * its file without a copy, src/model_file.mm:89-100; MI355X has to upload it, and does so into
+ * the layout its kernels stream best). For T = ceil(N/16) tiles of 16 rows, G = K/64 groups
+ * padded to G4 = ceil(G/4) quads, and group pairs p (groups 2p, 2p+1):
+ *   codes:       T*2*G4 kilobytes; the kilobyte of (tile t, pair p) holds, for lane l = 16j + c
+ *                (j = 0..3, c = 0..15), four uint32 words of row 16t + c: word 8g + 4s + j for
+ *                (g, s) = (2p,0), (2p,1), (2p+1,0), (2p+1,1), in MLX nibble order (element k at
+ *                bits 4*(k%8) of word k/8);
+ *   scale/bias:  after the codes, T*G4*16 entries of 16 bytes, ((t*G4 + q)*16 + c): for groups
+ *                4q .. 4q+3, s bits | b bits << 16;
+ * rows beyond N and groups beyond G are zero. Total rlq_packed_affine_bytes(K, N) =
+ * T*G4*2304 bytes: exactly K*N/2 + 4*N*K/64 when N % 16 == 0 and K % 256 == 0. */
+size_t rlq_packed_affine_bytes(int K, int N);
+
+/* MLX layout -> packed. Replaces the affine part of tools/convert.py's pack_blocked
+ * (:92-117) as the producer of the kernels' layout. */
+int rlq_pack_affine(const uint32_t *w, const void *s, const void *b, int K, int N, void *packed, void *stream);
+
+/* Blocked q4a file layout (tools/convert.py:92-117: bytes [n_pad/256][K][128], 16-bit s and b
+ * [n_pad/256][K/64][256]) rows [row0, row0+rows) -> packed matrix of N = rows, e.g. one part of
+ * a stacked tensor (src/model_file.h:52, QTensor::parts). */
+int rlq_pack_affine_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const uint16_t *b_blk,
+                            int K, int n_pad, int row0, int rows, void *packed, void *stream);
+
+/* Blocked q4a file layout -> MLX layout (the interchange format), rows [row0, row0+rows). */
+int rlq_repack_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const uint16_t *b_blk,
+                       int K, int n_pad, int row0, int rows,
+                       uint32_t *w, uint16_t *s, uint16_t *b, void *stream);
+
 /* ---------------------------------------------------------------- dense affine linear */
 
-/* Bytes of scratch rlq_linear_affine needs for these sizes (0 if none). The scratch must
- * be zero-filled once when it is allocated (rlq_workspace_clear); calls leave it zeroed. */
+/* Bytes of scratch rlq_linear_affine needs for these sizes. The scratch must be zero-filled
+ * once when it is allocated (rlq_workspace_clear); calls leave its counter area zeroed. */
 size_t rlq_linear_workspace_bytes(int M, int K, int N);
 int rlq_workspace_clear(void *workspace, size_t bytes, void *stream);
 
 /* y[m][n] = sum_k x[m][k] * W[n][k]   (accum = 0)
  * y[m][n] += that                      (accum = 1: the residual add, ACCUM in the reference)
- * x: fp16 [M][x_stride]; W as above; y: fp32 [M][y_stride]. K % 64 == 0, M >= 1, N >= 1.
+ * x: fp16 [M][x_stride]; W packed as above; y: fp32 [M][y_stride]. K % 64 == 0, M, N >= 1.
  * Replaces group_sums + linear_q4a (kernels/linear.metal:34-116, dispatched by
- * src/engine.mm:875-905). M <= 32 runs the decode kernel (MFMA GEMV, split-K), larger M
- * the prefill kernel (LDS-staged MFMA GEMM). */
+ * src/engine.mm:875-905). M <= 8 runs the decode kernel (MFMA GEMV), larger M the prefill
+ * kernel (LDS-staged MFMA GEMM). */
 int rlq_linear_affine(const void *x, int x_stride, int M, int K, int N,
-                      const uint32_t *w, const void *s, const void *b, int scale_dtype,
+                      const void *packed, int scale_dtype,
                       float *y, int y_stride, int accum,
                       void *workspace, size_t workspace_bytes, void *stream);
 
-/* Forces one kernel family for tests and measurement: 0 = automatic, 1 = decode GEMV,
- * 2 = prefill GEMM. Same contract as rlq_linear_affine. */
+/* Forces one kernel family for tests and measurement: 0 = automatic, 1 = decode GEMV
+ * (M <= 8), 2 = prefill GEMM. Same contract as rlq_linear_affine. */
 int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int K, int N,
-                             const uint32_t *w, const void *s, const void *b, int scale_dtype,
+                             const void *packed, int scale_dtype,
                              float *y, int y_stride, int accum,
                              void *workspace, size_t workspace_bytes, void *stream);
 
-/* gsum[m][g] = sum_{k<64} x[m][64g+k] in fp32 (kernels/linear.metal:34-45). gsum: [M][K/64]. */
+/* gsum[m][g] = sum_{k<64} x[m][64g+k], summed in order in fp32 (kernels/linear.metal:34-45). */
 int rlq_group_sums(const void *x, int x_stride, int M, int K, float *gsum, void *stream);
 
-/* W[n][k] as fp32 [N][K], bit-exact to float(s)*q + float(b). A checking entry point: the
- * matmuls never materialise W. */
-int rlq_dequant_affine(const uint32_t *w, const void *s, const void *b, int scale_dtype,
-                       int K, int N, float *out, void *stream);
-
-/* Blocked q4a file layout (tools/convert.py:92-117: bytes [n_pad/256][K][128], 16-bit s and b
- * [n_pad/256][K/64][256]) -> MLX affine layout for rows [row0, row0+rows), e.g. one part of a
- * stacked tensor. The one-time upload repack (the reference maps the file without a copy,
- * src/model_file.mm:89-100; MI355X has to upload it, and does so into the kernels' layout). */
-int rlq_repack_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const uint16_t *b_blk,
-                       int K, int n_pad, int row0, int rows,
-                       uint32_t *w, uint16_t *s, uint16_t *b, void *stream);
+/* W[n][k] as fp32 [N][K] from a packed matrix, bit-exact to float(s)*q + float(b). A checking
+ * entry point: the matmuls never materialise W. */
+int rlq_dequant_affine(const void *packed, int scale_dtype, int K, int N, float *out, void *stream);
 
 #ifdef __cplusplus
 }

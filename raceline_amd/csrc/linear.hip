@@ -1,5 +1,5 @@
-// Affine 4-bit group-quantized linear layer on gfx950: decode GEMV, prefill GEMM,
-// group sums, a dequantizing check kernel and the blocked->MLX upload repack.
+// Affine 4-bit group-quantized linear layer on gfx950: the packed device layout and its
+// upload kernels, the decode GEMV, the prefill GEMM, group sums and a dequantizing check.
 //
 //   y[m][n] = sum_k x[m][k] * W[n][k],   W[n][k] = s[n][g] * q[n][k] + b[n][g],  g = k / 64
 //
@@ -9,14 +9,25 @@
 // matrix cores as exact fp16 values and the scale and bias are applied per group
 // to the fp32 partial product.
 //
-// Matrix-core operand layout (v_mfma_f32_32x32x16_f16, wave64):
-//   A (32 x 16): lane l holds row l%32, k = 8*(l/32) .. +7
-//   B (16 x 32): lane l holds col l%32, k = 8*(l/32) .. +7
-//   D (32 x 32): lane l, element v holds col l%32, row 8*(v/4) + 4*(l/32) + v%4
-// A is the activations (rows = tokens), B the weights (cols = output features). Per
-// group of 64 the lane with k-half h = l/32 feeds the four 8-element chunks
-// k = 32h + 8t (t = 0..3) of one 16-byte load of its weight row, so one group is four
-// MFMAs and each weight row is read as 32 contiguous bytes per group.
+// Matrix cores: v_mfma_f32_16x16x32_f16 (wave64), A = activations (rows = tokens), B =
+// codes (cols = output features):
+//   A (16 x 32): lane l holds row l%16, k = 8*(l/16) .. +7
+//   B (32 x 16): lane l holds col l%16, k = 8*(l/16) .. +7
+//   D (16 x 16): lane l holds col l%16, rows 4*(l/16) .. +3
+// One group of 64 inputs is two MFMA steps s = 0, 1 (k = 64g + 32s .. +31); lane (c, j) =
+// (l%16, l/16) feeds uint32 word 8g + 4s + j of row c (k = 64g + 32s + 8j .. +7).
+//
+// Packed device layout (made once at upload, from the MLX layout or the .rlm blocked
+// layout; see include/rlq.h), for tiles t of 16 output rows, G = K/64 groups padded to
+// G4 = ceil(G/4) quads, and group pairs p (groups 2p, 2p+1):
+//   codes: 1024 bytes per (t, p) at ((t*2*G4 + p) * 64 + l) * 16: lane l = 16j + c holds
+//          words (8g + 4s + j of row 16t + c) for (g, s) = (2p,0), (2p,1), (2p+1,0), (2p+1,1)
+//          (tools/convert.py:82-89 nibble order);
+//   scale/bias: after the codes, 16 bytes per (t, quad q, row c) at ((t*G4 + q)*16 + c)*16:
+//          s | b << 16 for groups 4q .. 4q+3;
+// rows beyond N and groups beyond G zero. One 16-byte load per lane brings a lane its
+// operands for two groups, and a wave's loads for consecutive group pairs are
+// consecutive kilobytes: a plain stream for the memory system.
 #include "rlq_common.h"
 #include "../../include/rlq.h"
 
@@ -25,430 +36,100 @@
 namespace rlq {
 
 constexpr int kGroup = 64;
-constexpr int kGemvMaxGps = 128;  // groups of one split of the decode kernel (LDS bound)
 
-// Workspace layout: a fixed area of split-K counters first (kept zero between calls, so it
-// must not move with the shape of a call), then the per-call scratch (partials, group sums).
-constexpr int kMaxTiles = 16384;                                   // N <= 32 * kMaxTiles
-constexpr size_t kCounterBytes = (size_t)kMaxTiles * sizeof(unsigned);
+// Workspace layout: a fixed area of counters first (kept zero between calls, so it must
+// not move with the shape of a call), then the per-call scratch (group sums).
+constexpr int kMaxTiles = 32768;                                   // N <= 16 * kMaxTiles
+constexpr size_t kCounterBytes = 65536;
 
-// ================================================================== decode GEMV (M <= 32)
-//
-// Grid (ceil(N/32), ksplit); 256 threads = 4 waves. A workgroup owns 32 output
-// features and `gps` consecutive groups of K; its four waves take consecutive quarters
-// of those groups, and their partial sums meet in LDS in a fixed order. When K is split
-// over workgroups (small N: the GPU needs >= ~1000 workgroups to fill 256 CUs), each
-// writes its partial [split][M][N] to the workspace and the last one to finish a column
-// tile (a counter per tile) adds them in split order and writes y. The order of every
-// sum depends only on (K, N), never on M or on timing, so a token's result is the same
-// whatever other tokens share the call.
-struct GemvArgs {
-  const _Float16 *x;
-  const uint32_t *w;
-  const uint16_t *s;
-  const uint16_t *b;
-  float *y;
-  float *part;
-  unsigned *counters;
-  int x_stride, M, K, N, y_stride;
-  int ksplit, gps;
-};
+__host__ __device__ inline int tiles_of(int N) { return (N + 15) / 16; }
+__host__ __device__ inline int quads_of(int K) { return (K / kGroup + 3) / 4; }
+static inline size_t packed_code_bytes(int K, int N) { return (size_t)tiles_of(N) * quads_of(K) * 2048; }
+static inline size_t packed_bytes(int K, int N) { return (size_t)tiles_of(N) * quads_of(K) * 2304; }
 
-template <int NV, int SD, bool ACC>
-__global__ __launch_bounds__(256) void gemv_q4a_kernel(GemvArgs a) {
-  constexpr int MT = 8 * NV;  // token rows covered: acc quads 0..NV-1
-  __shared__ __attribute__((aligned(16))) float gs[kGemvMaxGps][MT];
-  __shared__ __attribute__((aligned(16))) float red[3][64][4 * NV];
-  __shared__ int last;
+// ================================================================== packing (upload)
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int h = lane >> 5, col = lane & 31;
-  const int n0 = blockIdx.x * 32;
-  const int n = n0 + col;
-  const bool nvalid = n < a.N;
-  const int G = a.K / kGroup;
-  const int g0 = blockIdx.y * a.gps;
-  const int g1 = min(G, g0 + a.gps);
-  const int ng = g1 - g0;
-
-  // Group sums of the activations over this split's groups, summed sequentially in
-  // fp32 as group_sums does (kernels/linear.metal:34-45). Rows >= M are zero.
-  for (int idx = tid; idx < MT * ng; idx += 256) {
-    const int m = idx / ng, gl = idx - m * ng;
-    float sum = 0.0f;
-    if (m < a.M) {
-      const half8 *xp = reinterpret_cast<const half8 *>(a.x + (size_t)m * a.x_stride + (size_t)(g0 + gl) * kGroup);
+// MLX layout (codes uint32 [N][K/8], scales and biases [N][G]) -> packed. One thread per
+// 16-byte piece of codes (tile t, pair p, lane l); threads of lane < 16 of even pairs
+// also write the scale/bias quad of their row.
+__global__ void pack_mlx_kernel(const uint32_t *w, const uint16_t *s, const uint16_t *b, int K, int N,
+                                u32x4 *codes, u32x4 *sb) {
+  const int G = K / kGroup, G4 = quads_of(K), GP = 2 * G4;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;   // ((t * GP + p) * 64 + l)
+  if (i >= (size_t)tiles_of(N) * GP * 64) return;
+  const int l = (int)(i & 63);
+  const size_t tp = i >> 6;
+  const int t = (int)(tp / GP), p = (int)(tp - (size_t)t * GP);
+  const int c = l & 15, j = l >> 4, n = 16 * t + c;
+  u32x4 v = {};
+  if (n < N) {
+    const uint32_t *row = w + (size_t)n * (K / 8);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const half8 v = xp[c];
+    for (int e = 0; e < 4; ++e) {
+      const int g = 2 * p + (e >> 1), sx = e & 1;
+      v[e] = g < G ? row[8 * g + 4 * sx + j] : 0u;
+    }
+  }
+  codes[i] = v;
+  if (j == 0 && (p & 1) == 0) {
+    const int q = p >> 1;
+    u32x4 e4 = {};
+    if (n < N) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sum += static_cast<float>(v[e]);
+      for (int e = 0; e < 4; ++e) {
+        const int g = 4 * q + e;
+        e4[e] = g < G ? ((uint32_t)s[(size_t)n * G + g] | ((uint32_t)b[(size_t)n * G + g] << 16)) : 0u;
       }
     }
-    gs[gl][m] = sum;
-  }
-  __syncthreads();
-
-  const int wpg = (ng + 3) >> 2;
-  const int wg0 = g0 + wave * wpg;
-  const int wg1 = min(g1, wg0 + wpg);
-
-  const uint32_t *wrow = a.w + (size_t)(nvalid ? n : 0) * (a.K / 8) + 4 * h;
-  const bool xvalid = col < a.M;
-  const _Float16 *xrow = a.x + (size_t)(xvalid ? col : 0) * a.x_stride + 32 * h;
-  const uint16_t *srow = a.s + (size_t)(nvalid ? n : 0) * G;
-  const uint16_t *brow = a.b + (size_t)(nvalid ? n : 0) * G;
-
-  f32x16 acc = {};
-  const half8 hz = {};
-
-  auto group_step = [&](int g, u32x4 wq, const half8 *xa) {
-    f32x16 p = {};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) p = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[t], nib8_to_half8(wq[t]), p, 0, 0, 0);
-    const float sc = nvalid ? scale_f32<SD>(srow[g]) * kTwo24 : 0.0f;
-    const float bi = nvalid ? scale_f32<SD>(brow[g]) : 0.0f;
-    const float *gsg = gs[g - g0];
-#pragma unroll
-    for (int q = 0; q < NV; ++q) {
-      const f32x4 gq = *reinterpret_cast<const f32x4 *>(gsg + 8 * q + 4 * h);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[4 * q + r] += sc * p[4 * q + r] + bi * gq[r];
-    }
-  };
-
-  int g = wg0;
-  for (; g + 4 <= wg1; g += 4) {
-    u32x4 wq[4];
-    half8 xa[4][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) wq[j] = nvalid ? *reinterpret_cast<const u32x4 *>(wrow + 8 * (g + j)) : u32x4{};
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        xa[j][t] = xvalid ? *reinterpret_cast<const half8 *>(xrow + kGroup * (g + j) + 8 * t) : hz;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) group_step(g + j, wq[j], xa[j]);
-  }
-  for (; g < wg1; ++g) {
-    const u32x4 wq = nvalid ? *reinterpret_cast<const u32x4 *>(wrow + 8 * g) : u32x4{};
-    half8 xa[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) xa[t] = xvalid ? *reinterpret_cast<const half8 *>(xrow + kGroup * g + 8 * t) : hz;
-    group_step(g, wq, xa);
-  }
-
-  // Waves 1..3 hand their partials to wave 0, which adds them in wave order.
-  if (wave > 0) {
-#pragma unroll
-    for (int v = 0; v < 4 * NV; ++v) red[wave - 1][lane][v] = acc[v];
-  }
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int w = 0; w < 3; ++w)
-#pragma unroll
-      for (int v = 0; v < 4 * NV; ++v) acc[v] += red[w][lane][v];
-  }
-
-  if (a.ksplit == 1) {
-    if (wave == 0 && nvalid) {
-#pragma unroll
-      for (int v = 0; v < 4 * NV; ++v) {
-        const int m = 8 * (v >> 2) + 4 * h + (v & 3);
-        if (m < a.M) {
-          float *dst = a.y + (size_t)m * a.y_stride + n;
-          *dst = ACC ? *dst + acc[v] : acc[v];
-        }
-      }
-    }
-    return;
-  }
-
-  // Split K: publish this split's partial, then count it. The partials are agent-scope
-  // atomic stores (coherent across the XCDs' L2s) and the wave waits for them to complete
-  // before the counter moves, so the last workgroup, reading them with agent-scope atomic
-  // loads, sees every one. No fence: an agent-scope fence writes back and invalidates the
-  // whole L2, which serialises thousands of workgroups.
-  float *P = a.part + (size_t)blockIdx.y * a.M * a.N;
-  if (wave == 0) {
-    if (nvalid) {
-#pragma unroll
-      for (int v = 0; v < 4 * NV; ++v) {
-        const int m = 8 * (v >> 2) + 4 * h + (v & 3);
-        if (m < a.M) __hip_atomic_store(P + (size_t)m * a.N + n, acc[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (tid == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(a.counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-      last = (prev == (unsigned)(a.ksplit - 1));
-    }
-  }
-  __syncthreads();
-  if (!last) return;
-  for (int idx = tid; idx < a.M * 32; idx += 256) {
-    const int m = idx >> 5, nn = n0 + (idx & 31);
-    if (nn >= a.N) continue;
-    float sum = 0.0f;
-    const float *src = a.part + (size_t)m * a.N + nn;
-    for (int sp = 0; sp < a.ksplit; ++sp)
-      sum += __hip_atomic_load(src + (size_t)sp * a.M * a.N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    float *dst = a.y + (size_t)m * a.y_stride + nn;
-    *dst = ACC ? *dst + sum : sum;
-  }
-  if (tid == 0) __hip_atomic_store(a.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Split of K over workgroups for the decode kernel. A function of (K, N) only, so the
-// summation order of an output never depends on M.
-struct GemvPlan {
-  int ntiles, ksplit, gps;
-};
-
-static GemvPlan gemv_plan(int K, int N) {
-  GemvPlan p;
-  const int G = K / kGroup;
-  p.ntiles = (N + 31) / 32;
-  int ks = std::max(1, (1024 + p.ntiles - 1) / p.ntiles);
-  ks = std::min(ks, std::max(1, G / 4));
-  ks = std::max(ks, (G + kGemvMaxGps - 1) / kGemvMaxGps);
-  int gps = (G + ks - 1) / ks;
-  gps = (gps + 3) / 4 * 4;
-  gps = std::min(gps, kGemvMaxGps);
-  p.gps = gps;
-  p.ksplit = (G + gps - 1) / gps;
-  return p;
-}
-
-static size_t gemv_workspace(int M, int K, int N) {
-  const GemvPlan p = gemv_plan(K, N);
-  if (p.ksplit == 1) return 0;
-  return kCounterBytes + (size_t)p.ksplit * M * N * sizeof(float);
-}
-
-template <int SD, bool ACC>
-static void launch_gemv(int nv, dim3 grid, hipStream_t st, const GemvArgs &a) {
-  switch (nv) {
-    case 1: gemv_q4a_kernel<1, SD, ACC><<<grid, 256, 0, st>>>(a); break;
-    case 2: gemv_q4a_kernel<2, SD, ACC><<<grid, 256, 0, st>>>(a); break;
-    case 3: gemv_q4a_kernel<3, SD, ACC><<<grid, 256, 0, st>>>(a); break;
-    default: gemv_q4a_kernel<4, SD, ACC><<<grid, 256, 0, st>>>(a); break;
+    sb[((size_t)t * G4 + q) * 16 + c] = e4;
   }
 }
 
-static int run_gemv(const _Float16 *x, int x_stride, int M, int K, int N, const uint32_t *w, const uint16_t *s,
-                    const uint16_t *b, int sd, float *y, int y_stride, int accum, void *ws, size_t ws_bytes,
-                    hipStream_t st) {
-  RLQ_REQUIRE(M <= 32, "decode kernel handles M <= 32 rows (got %d)", M);
-  const GemvPlan p = gemv_plan(K, N);
-  const size_t need = gemv_workspace(M, K, N);
-  RLQ_REQUIRE(ws_bytes >= need, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
-  RLQ_REQUIRE(need == 0 || aligned(ws, 16), "workspace must be 16-byte aligned");
-  GemvArgs a;
-  a.x = x; a.w = w; a.s = s; a.b = b; a.y = y;
-  a.counters = static_cast<unsigned *>(ws);
-  a.part = need ? reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterBytes) : nullptr;
-  a.x_stride = x_stride; a.M = M; a.K = K; a.N = N; a.y_stride = y_stride;
-  a.ksplit = p.ksplit; a.gps = p.gps;
-  const int nv = (M + 7) / 8;
-  const dim3 grid(p.ntiles, p.ksplit);
-  if (sd == RLQ_F16) {
-    if (accum) launch_gemv<0, true>(nv, grid, st, a); else launch_gemv<0, false>(nv, grid, st, a);
-  } else {
-    if (accum) launch_gemv<1, true>(nv, grid, st, a); else launch_gemv<1, false>(nv, grid, st, a);
-  }
-  RLQ_HIP(hipGetLastError());
-  return 0;
-}
-
-// ================================================================== group sums
-
-// gsum[m][g] (row stride gs_stride) and, when gsT != null, the transpose gsT[g][m_pad].
-__global__ void group_sums_kernel(const _Float16 *x, int x_stride, int M, int K, float *gsum, float *gsT, int m_pad) {
-  const int G = K / kGroup;
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= M * G) return;
-  const int m = idx / G, g = idx - m * G;
-  const half8 *xp = reinterpret_cast<const half8 *>(x + (size_t)m * x_stride + (size_t)g * kGroup);
-  float sum = 0.0f;
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const half8 v = xp[c];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sum += static_cast<float>(v[e]);
-  }
-  if (gsum) gsum[(size_t)m * G + g] = sum;
-  if (gsT) gsT[(size_t)g * m_pad + m] = sum;
-}
-
-// ================================================================== prefill GEMM (M > 32)
-//
-// Workgroup tile 128 (tokens) x 128 (features), 4 waves as 2 x 2, each 64 x 64 = 2 x 2
-// MFMA tiles. Per group of 64: the activation tile goes through LDS (shared by the two
-// waves of a row band); each wave loads its own 64 weight rows' 32 bytes straight into
-// B operands and turns them into exact fp16 codes in registers; four MFMAs per tile
-// give the group's partial product, then acc += s * part + b * gsum.
-struct GemmArgs {
-  const _Float16 *x;
-  const uint32_t *w;
-  const uint16_t *s;
-  const uint16_t *b;
-  const float *gsT;  // [G][m_pad]
-  float *y;
-  int x_stride, M, K, N, y_stride, m_pad;
-};
-
-constexpr int kBM = 128, kBN = 128, kLdsRow = 64 + 8;
-
-template <int SD, bool ACC>
-__global__ __launch_bounds__(256) void gemm_q4a_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[kBM * kLdsRow];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int h = lane >> 5, col = lane & 31;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-  const int G = a.K / kGroup;
-
-  int nrow[2];
-  bool nval[2];
-  const uint32_t *wr[2];
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    nrow[ct] = n0 + wn * 64 + ct * 32 + col;
-    nval[ct] = nrow[ct] < a.N;
-    wr[ct] = a.w + (size_t)(nval[ct] ? nrow[ct] : 0) * (a.K / 8) + 4 * h;
-  }
-
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-  for (int g = 0; g < G; ++g) {
-    // activation tile [128][64] -> LDS: 1024 chunks of 8 halves, 4 per thread
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int chunk = tid + 256 * c;
-      const int r = chunk >> 3, kc = chunk & 7;
-      const int m = m0 + r;
-      half8 v = {};
-      if (m < a.M) v = *reinterpret_cast<const half8 *>(a.x + (size_t)m * a.x_stride + (size_t)g * kGroup + 8 * kc);
-      *reinterpret_cast<half8 *>(As + r * kLdsRow + 8 * kc) = v;
-    }
-    u32x4 wq[2];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) wq[ct] = nval[ct] ? *reinterpret_cast<const u32x4 *>(wr[ct] + 8 * g) : u32x4{};
-    __syncthreads();
-
-    half8 bf[2][4];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) bf[ct][t] = nib8_to_half8(wq[ct][t]);
-
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      half8 af[4];
-      const _Float16 *arow = As + (wm * 64 + rt * 32 + col) * kLdsRow + 32 * h;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) af[t] = *reinterpret_cast<const half8 *>(arow + 8 * t);
-      const f32x4 *gsp = reinterpret_cast<const f32x4 *>(a.gsT + (size_t)g * a.m_pad + m0 + wm * 64 + rt * 32 + 4 * h);
-      f32x4 gq[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) gq[q] = gsp[2 * q];
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        f32x16 p = {};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) p = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[t], bf[ct][t], p, 0, 0, 0);
-        const float sc = nval[ct] ? scale_f32<SD>(a.s[(size_t)nrow[ct] * G + g]) * kTwo24 : 0.0f;
-        const float bi = nval[ct] ? scale_f32<SD>(a.b[(size_t)nrow[ct] * G + g]) : 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[rt][ct][4 * q + r] += sc * p[4 * q + r] + bi * gq[q][r];
-      }
-    }
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      if (!nval[ct]) continue;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * 64 + rt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (m < a.M) {
-          float *dst = a.y + (size_t)m * a.y_stride + nrow[ct];
-          *dst = ACC ? *dst + acc[rt][ct][v] : acc[rt][ct][v];
-        }
-      }
-    }
-}
-
-static size_t gemm_workspace(int M, int K) {
-  const int m_pad = (M + kBM - 1) / kBM * kBM;
-  return kCounterBytes + (size_t)(K / kGroup) * m_pad * sizeof(float);
-}
-
-static int run_gemm(const _Float16 *x, int x_stride, int M, int K, int N, const uint32_t *w, const uint16_t *s,
-                    const uint16_t *b, int sd, float *y, int y_stride, int accum, void *ws, size_t ws_bytes,
-                    hipStream_t st) {
-  const size_t need = gemm_workspace(M, K);
-  RLQ_REQUIRE(ws_bytes >= need, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
-  RLQ_REQUIRE(aligned(ws, 16), "workspace must be 16-byte aligned");
-  const int m_pad = (M + kBM - 1) / kBM * kBM;
-  float *gsT = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterBytes);
-  // rows M..m_pad of gsT are never read for output rows >= M; they only need to be finite
-  const int G = K / kGroup;
-  group_sums_kernel<<<(M * G + 255) / 256, 256, 0, st>>>(x, x_stride, M, K, nullptr, gsT, m_pad);
-  RLQ_HIP(hipGetLastError());
-  GemmArgs a;
-  a.x = x; a.w = w; a.s = s; a.b = b; a.gsT = gsT; a.y = y;
-  a.x_stride = x_stride; a.M = M; a.K = K; a.N = N; a.y_stride = y_stride; a.m_pad = m_pad;
-  const dim3 grid((N + kBN - 1) / kBN, m_pad / kBM);
-  if (sd == RLQ_F16) {
-    if (accum) gemm_q4a_kernel<0, true><<<grid, 256, 0, st>>>(a);
-    else gemm_q4a_kernel<0, false><<<grid, 256, 0, st>>>(a);
-  } else {
-    if (accum) gemm_q4a_kernel<1, true><<<grid, 256, 0, st>>>(a);
-    else gemm_q4a_kernel<1, false><<<grid, 256, 0, st>>>(a);
-  }
-  RLQ_HIP(hipGetLastError());
-  return 0;
-}
-
-// ================================================================== dequant (checking)
-
-template <int SD>
-__global__ void dequant_kernel(const uint32_t *w, const uint16_t *s, const uint16_t *b, int K, int N, float *out) {
-  const size_t words = (size_t)N * (K / 8);
+// Blocked q4a file layout (tools/convert.py:92-117) rows [row0, row0 + rows) -> packed.
+// The file stores, per block of 256 rows and input index k, 128 bytes with row 2i in the
+// low and row 2i+1 in the high nibble of byte i.
+__global__ void pack_blocked_kernel(const uint8_t *w_blk, const uint16_t *s_blk, const uint16_t *b_blk, int K,
+                                    int row0, int rows, u32x4 *codes, u32x4 *sb) {
+  const int G = K / kGroup, G4 = quads_of(K), GP = 2 * G4;
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= words) return;
-  const int n = (int)(i / (K / 8));
-  const int c = (int)(i - (size_t)n * (K / 8));
-  const int g = (8 * c) / kGroup;
-  const float sc = scale_f32<SD>(s[(size_t)n * (K / kGroup) + g]);
-  const float bi = scale_f32<SD>(b[(size_t)n * (K / kGroup) + g]);
-  const uint32_t u = w[i];
-  float *o = out + (size_t)n * K + 8 * c;
+  if (i >= (size_t)tiles_of(rows) * GP * 64) return;
+  const int l = (int)(i & 63);
+  const size_t tp = i >> 6;
+  const int t = (int)(tp / GP), p = (int)(tp - (size_t)t * GP);
+  const int c = l & 15, j = l >> 4, r = 16 * t + c;
+  u32x4 v = {};
+  const int n = row0 + r, blk = n >> 8, cb = n & 255;
+  if (r < rows) {
+    const int shift = (cb & 1) ? 4 : 0;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = __fmaf_rn(sc, (float)((u >> (4 * e)) & 15u), bi);
+    for (int e = 0; e < 4; ++e) {
+      const int g = 2 * p + (e >> 1), sx = e & 1;
+      uint32_t u = 0;
+      if (g < G) {
+        const uint8_t *src = w_blk + ((size_t)blk * K + 64 * g + 32 * sx + 8 * j) * 128 + (cb >> 1);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) u |= ((uint32_t)(src[(size_t)k * 128] >> shift) & 15u) << (4 * k);
+      }
+      v[e] = u;
+    }
+  }
+  codes[i] = v;
+  if (j == 0 && (p & 1) == 0) {
+    const int q = p >> 1;
+    u32x4 e4 = {};
+    if (r < rows) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int g = 4 * q + e;
+        const size_t o = ((size_t)blk * G + g) * 256 + cb;
+        e4[e] = g < G ? ((uint32_t)s_blk[o] | ((uint32_t)b_blk[o] << 16)) : 0u;
+      }
+    }
+    sb[((size_t)t * G4 + q) * 16 + c] = e4;
+  }
 }
 
-// ================================================================== blocked -> MLX repack
-
+// Blocked file layout -> MLX layout (the interchange format), rows [row0, row0 + rows).
 __global__ void repack_w_kernel(const uint8_t *w_blk, int K, int row0, int rows, uint32_t *w) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int words = K / 8;
@@ -476,17 +157,500 @@ __global__ void repack_sb_kernel(const uint16_t *s_blk, const uint16_t *b_blk, i
   b[i] = b_blk[src];
 }
 
-static int check_linear_args(const char *fn, const void *x, int x_stride, int M, int K, int N, const uint32_t *w,
-                             const void *s, const void *b, int sd, const float *y, int y_stride) {
+// ================================================================== dequant (checking)
+
+template <int SD>
+__global__ void dequant_kernel(const u32x4 *codes, const u32x4 *sb, int K, int N, float *out) {
+  const int G = K / kGroup, G4 = quads_of(K), GP = 2 * G4;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)tiles_of(N) * GP * 64) return;
+  const int l = (int)(i & 63);
+  const size_t tp = i >> 6;
+  const int t = (int)(tp / GP), p = (int)(tp - (size_t)t * GP);
+  const int c = l & 15, j = l >> 4, n = 16 * t + c;
+  if (n >= N) return;
+  const u32x4 v = codes[i];
+  const u32x4 q4 = sb[((size_t)t * G4 + (p >> 1)) * 16 + c];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int g = 2 * p + (e >> 1), sx = e & 1;
+    if (g >= G) continue;
+    const uint32_t pr = q4[2 * (p & 1) + (e >> 1)];
+    const float sc = scale_f32<SD>((uint16_t)(pr & 0xFFFF));
+    const float bi = scale_f32<SD>((uint16_t)(pr >> 16));
+    float *o = out + (size_t)n * K + 64 * g + 32 * sx + 8 * j;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = __fmaf_rn(sc, (float)((v[e] >> (4 * k)) & 15u), bi);
+  }
+}
+
+// ================================================================== decode GEMV (M <= 8)
+//
+// Grid: one workgroup per tile of 16 output features; W = ceil(groups / GPW) waves (at
+// most 16; GPW in {16, 24} groups per wave, a function of K only) split the K groups into
+// consecutive ranges, and their partial sums meet in LDS in wave order. No split of K
+// across workgroups: every output is written by the workgroup that owns it, and the
+// order of every sum depends only on K, never on M or on timing, so a token's result is
+// the same whatever other tokens share the call.
+//
+// Each wave is single-shot, like a streaming copy: it issues every load of its range at
+// once (the codes as one 16-byte load per lane per group pair: a contiguous kilobyte per
+// wave instruction; the scale/bias quads; the activations), then multiplies and exits.
+// Latency is hidden by the many short-lived waves the hardware keeps in flight, not by a
+// software pipeline. Loads go through buffer descriptors whose range check returns zero
+// past the end of a wave's range, so the code is straight-line. Codes and scales are read
+// non-temporally (they are used once).
+//
+// One token (M = 1): each wave stages its activation range in LDS, in operand order.
+// Several tokens: lanes read their activation operands straight from memory (L2-resident,
+// shared by every workgroup) and reorder them in registers. Either way the group sums
+// come from an MFMA against a constant operand, which lands them in the accumulator
+// layout, and every weight load of a wave is issued before its first multiply.
+//
+// Operand trick: a uint32 of eight codes becomes four fp16 pairs with five ops,
+//   d0 = u & 0x000F000F -> (q0, q4)          d1 = u & 0x00F000F0 -> (16 q1, 16 q5)
+//   d2 = (u>>8) & 0x000F000F -> (q2, q6)     d3 = (u>>8) & 0x00F000F0 -> (16 q3, 16 q7)
+// each half being the subnormal (code or 16 * code) * 2^-24, exact. The activation
+// operand carries the same element order with the odd elements divided by 16:
+//   (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16),
+// so one MFMA step sums x_e * q_e * 2^-24 over the eight elements. (x/16 is exact unless
+// |x| < 2^-10, where it rounds to the fp16 subnormal grid: an error below 2^-25 * 16 * 15
+// per such element, far under the 1e-3 bar.) The accumulator carries the same 2^-24:
+// acc += s * part + b * (gsum * 2^-24), both exact rescalings, and is multiplied by 2^24
+// once at the end.
+constexpr int kGemvMaxM = 8;
+constexpr int kBufFlags = 0x00020000;             // buffer descriptor word 3 for raw 32-bit accesses
+constexpr int kNonTemporal = 2;                   // buffer load cache policy: stream, do not keep
+constexpr float kTwoM24 = 5.9604644775390625e-8f; // 2^-24
+
+struct GemvArgs {
+  const _Float16 *x;
+  const u32x4 *codes;
+  const u32x4 *sb;
+  float *y;
+  int x_stride, M, K, N, y_stride;
+};
+
+__device__ __forceinline__ half8 nib8_to_half8_oddx16(uint32_t u) {
+  const uint32_t t = u >> 8;
+  u32x4 d;
+  d[0] = u & 0x000F000Fu;
+  d[1] = u & 0x00F000F0u;
+  d[2] = t & 0x000F000Fu;
+  d[3] = t & 0x00F000F0u;
+  return __builtin_bit_cast(half8, d);
+}
+
+// eight consecutive activations -> operand order (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16)
+__device__ __forceinline__ u32x4 prep_x8(u32x4 p) {
+  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  const half2v sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(p[2], p[0], 0x05040100u);  // (x0, x4)
+  r[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(p[2], p[0], 0x07060302u)) * sixteenth);
+  r[2] = __builtin_amdgcn_perm(p[3], p[1], 0x05040100u);  // (x2, x6)
+  r[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(p[3], p[1], 0x07060302u)) * sixteenth);
+  return r;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kBufFlags);
+}
+
+// acc += float(s16) * p with the 16-bit float taken from the low or high half of a packed pair
+template <int SD, int HI>
+__device__ __forceinline__ float fma_scale(uint32_t pr, float p, float acc) {
+  if constexpr (SD == 0) {
+    const _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)(HI ? (pr >> 16) : (pr & 0xFFFFu)));
+    return __builtin_fmaf(static_cast<float>(v), p, acc);
+  } else {
+    const float v = __uint_as_float(HI ? (pr & 0xFFFF0000u) : (pr << 16));
+    return __builtin_fmaf(v, p, acc);
+  }
+}
+
+// Groups per wave: 16, or 24 when 16 would need more than 16 waves.
+static int gemv_gpw(int K) { return 4 * quads_of(K) <= 16 * 16 ? 16 : 24; }
+static int gemv_waves(int K) { const int g = gemv_gpw(K); return (4 * quads_of(K) + g - 1) / g; }
+
+// the cross-wave reduction [waves-1][64][4] floats, then (M = 1) each wave's staged
+// activations [gpw * 64] halves
+static size_t gemv_lds_bytes(int M, int waves, int gpw) {
+  return (size_t)(waves - 1) * 64 * 16 + (M == 1 ? (size_t)waves * gpw * kGroup * 2 : 0);
+}
+
+// MAXM: 1 (single-token decode: one activation row, one live accumulator) or 8.
+template <int MAXM, int GPW, int SD, bool ACC>
+__global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int waves = blockDim.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar control flow
+  const int c16 = lane & 15, j4 = lane >> 4;
+  const int G = a.K / kGroup, G4 = quads_of(a.K);
+  const int t = blockIdx.x;
+  const int n = 16 * t + c16;
+  const int M = a.M;
+  float *red = reinterpret_cast<float *>(lds);                              // [waves-1][64][4]
+
+  // this wave's groups [wg0, wg0 + GPW) of the padded range; descriptors cover exactly
+  // its part of the packed matrix, so loads past the end return zeros
+  const int wg0 = wave * GPW;
+  const int wq1 = min(4 * G4, wg0 + GPW);
+  const int wn = max(0, min(G, wg0 + GPW) - wg0);       // real groups of this wave
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.codes + ((size_t)t * 2 * G4 + wg0 / 2) * 64, (uint32_t)(wq1 - wg0) / 2u * 1024u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sb + ((size_t)t * G4 + wg0 / 4) * 16, (uint32_t)(wq1 - wg0) / 4u * 256u);
+  const uint32_t xrange = wn > 0 ? (uint32_t)((M - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
+
+  u32x4 wq[GPW / 2], sq[GPW / 4];
+  auto issue_w = [&]() {
+#pragma unroll
+    for (int pp = 0; pp < GPW / 2; ++pp)
+      wq[pp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, 16u * lane, (uint32_t)pp * 1024u, kNonTemporal));
+#pragma unroll
+    for (int qq = 0; qq < GPW / 4; ++qq)
+      sq[qq] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16u * c16, (uint32_t)qq * 256u, kNonTemporal));
+  };
+
+  // The group sums come from an MFMA against the constant (2^-24, 2^-24, 16 * 2^-24,
+  // 16 * 2^-24, ...), which undoes the 1/16 of the odd elements. An MFMA output row depends
+  // only on its own operand row, so a token's result is the same for every M.
+  const half8 ones = __builtin_bit_cast(half8, u32x4{0x00010001u, 0x00100010u, 0x00010001u, 0x00100010u});
+  f32x4 acc = {};
+  auto step = [&](int jg, const half8 *af) {
+    f32x4 p = {}, gsv = {};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], nib8_to_half8_oddx16(wq[jg >> 1][2 * (jg & 1) + s]), p, 0, 0, 0);
+      gsv = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, gsv, 0, 0, 0);
+    }
+    const uint32_t pr = sq[jg >> 2][jg & 3];
+    // MAXM = 1: only token row 0 is live (lanes 0..15, element 0)
+#pragma unroll
+    for (int r = 0; r < (MAXM == 1 ? 1 : 4); ++r) acc[r] = fma_scale<SD, 1>(pr, gsv[r], fma_scale<SD, 0>(pr, p[r], acc[r]));
+  };
+
+  if constexpr (MAXM == 1) {
+    // One token: the wave's activation row is loaded first (the loads complete in issue
+    // order, so waiting for it does not wait for the weights), then every weight load is
+    // issued; the row is staged in LDS in operand order while the weights are in flight.
+    // Every lane reads row 0's operand: MFMA rows are independent and only row 0 of the
+    // result is kept, so no zero rows are needed.
+    constexpr int XCH = GPW * 8;                 // chunks of 8 activations in the wave's range
+    constexpr int XPER = (XCH + 63) / 64;
+    _Float16 *xs = reinterpret_cast<_Float16 *>(lds + (size_t)(waves - 1) * 64 * 16) + (size_t)wave * GPW * kGroup;
+    u32x4 xr[XPER];
+#pragma unroll
+    for (int i = 0; i < XPER; ++i) {
+      const int chunk = lane + 64 * i;
+      const bool in_range = chunk < XCH && (chunk >> 3) < wn;
+      xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, in_range ? 16u * chunk : 0x7FFFFFF0u, 0, 0));
+    }
+    issue_w();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < XPER; ++i) {
+      const int chunk = lane + 64 * i;
+      if (chunk < XCH) *reinterpret_cast<u32x4 *>(xs + 8 * chunk) = prep_x8(xr[i]);
+    }
+    // other lanes of this wave read what was just written: keep the LDS reads after the writes
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const _Float16 *xa = xs + 8 * j4;
+    half8 an[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) an[s] = *reinterpret_cast<const half8 *>(xa + 32 * s);
+#pragma unroll
+    for (int jg = 0; jg < GPW; ++jg) {
+      const half8 af[2] = {an[0], an[1]};
+      if (jg + 1 < GPW) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) an[s] = *reinterpret_cast<const half8 *>(xa + (jg + 1) * kGroup + 32 * s);
+      }
+      step(jg, af);
+      __builtin_amdgcn_sched_barrier(0);   // one group at a time: bounded register use
+    }
+  } else {
+    // Several tokens: activation operands come straight from memory (L2-resident, shared
+    // by every workgroup), two groups ahead, and are put in operand order in registers;
+    // lanes whose token row is >= M read zeros (out of the descriptor's range).
+    const bool live = c16 < M;
+    const uint32_t xoff = (uint32_t)c16 * a.x_stride * 2u + 16u * j4;
+    auto ldx = [&](int jg, int s) -> u32x4 {
+      const bool ok = live && jg < wn;
+      return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rx, ok ? xoff + (uint32_t)(jg * kGroup + 32 * s) * 2u : 0x7FFFFFF0u, 0, 0));
+    };
+    u32x4 ax[3][2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) ax[d][s] = ldx(d, s);
+    issue_w();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int jg = 0; jg < GPW; ++jg) {
+      if (jg + 2 < GPW) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) ax[(jg + 2) % 3][s] = ldx(jg + 2, s);
+      }
+      const half8 af[2] = {__builtin_bit_cast(half8, prep_x8(ax[jg % 3][0])),
+                           __builtin_bit_cast(half8, prep_x8(ax[jg % 3][1]))};
+      step(jg, af);
+    }
+  }
+
+  // waves 1.. hand their partials to wave 0, which adds them in wave order; lane (c16, j4)
+  // holds token rows 4 j4 .. 4 j4 + 3 of output n
+  if (wave > 0) *reinterpret_cast<f32x4 *>(red + ((wave - 1) * 64 + lane) * 4) = acc;
+  __syncthreads();
+  if (wave == 0 && n < a.N && 4 * j4 < M) {
+    for (int w = 1; w < waves; ++w) {
+      const f32x4 o = *reinterpret_cast<const f32x4 *>(red + ((w - 1) * 64 + lane) * 4);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] += o[v];
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * j4 + v;
+      if (m < M) {
+        float *dst = a.y + (size_t)m * a.y_stride + n;
+        const float val = acc[v] * kTwo24;
+        *dst = ACC ? *dst + val : val;
+      }
+    }
+  }
+}
+
+static size_t gemv_workspace(int, int, int) { return 0; }
+
+template <int MAXM, int GPW, int SD, bool ACC>
+static int launch_gemv_inst(dim3 grid, int threads, size_t lds, hipStream_t st, const GemvArgs &a) {
+  static bool attr_set = false;  // once per instance, before its first launch
+  if (!attr_set) {
+    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4a_kernel<MAXM, GPW, SD, ACC>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_set = true;
+  }
+  gemv_q4a_kernel<MAXM, GPW, SD, ACC><<<grid, threads, lds, st>>>(a);
+  return 0;
+}
+
+template <int MAXM, int GPW>
+static int launch_gemv(int sd, int accum, dim3 grid, int threads, size_t lds, hipStream_t st, const GemvArgs &a) {
+  if (sd == RLQ_F16)
+    return accum ? launch_gemv_inst<MAXM, GPW, 0, true>(grid, threads, lds, st, a)
+                 : launch_gemv_inst<MAXM, GPW, 0, false>(grid, threads, lds, st, a);
+  return accum ? launch_gemv_inst<MAXM, GPW, 1, true>(grid, threads, lds, st, a)
+               : launch_gemv_inst<MAXM, GPW, 1, false>(grid, threads, lds, st, a);
+}
+
+static int run_gemv(const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd, float *y,
+                    int y_stride, int accum, void *, size_t, hipStream_t st) {
+  RLQ_REQUIRE(M <= kGemvMaxM, "decode kernel handles M <= %d rows (got %d)", kGemvMaxM, M);
+  const int gpw = gemv_gpw(K), waves = gemv_waves(K);
+  RLQ_REQUIRE(waves <= 16, "decode kernel: K=%d is larger than the %d it supports", K, 16 * 24 * kGroup);
+  const size_t lds = gemv_lds_bytes(M, waves, gpw);
+  GemvArgs a;
+  a.x = x;
+  a.codes = static_cast<const u32x4 *>(packed);
+  a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
+  a.y = y;
+  a.x_stride = x_stride; a.M = M; a.K = K; a.N = N; a.y_stride = y_stride;
+  const dim3 grid(tiles_of(N));
+  const int threads = 64 * waves;
+  int rc;
+  if (M == 1) rc = gpw == 16 ? launch_gemv<1, 16>(sd, accum, grid, threads, lds, st, a)
+                             : launch_gemv<1, 24>(sd, accum, grid, threads, lds, st, a);
+  else rc = gpw == 16 ? launch_gemv<kGemvMaxM, 16>(sd, accum, grid, threads, lds, st, a)
+                      : launch_gemv<kGemvMaxM, 24>(sd, accum, grid, threads, lds, st, a);
+  if (rc) return rc;
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+// ================================================================== group sums
+
+// gsum[m][g] and/or its transpose gsT[g][m_pad], summed sequentially in fp32 as
+// group_sums does (kernels/linear.metal:34-45).
+__global__ void group_sums_kernel(const _Float16 *x, int x_stride, int M, int K, float *gsum, float *gsT, int m_pad) {
+  const int G = K / kGroup;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * G) return;
+  const int m = idx / G, g = idx - m * G;
+  const half8 *xp = reinterpret_cast<const half8 *>(x + (size_t)m * x_stride + (size_t)g * kGroup);
+  float sum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const half8 v = xp[c];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum += static_cast<float>(v[e]);
+  }
+  if (gsum) gsum[(size_t)m * G + g] = sum;
+  if (gsT) gsT[(size_t)g * m_pad + m] = sum;
+}
+
+// ================================================================== prefill GEMM (M > 8)
+//
+// Workgroup tile 128 (tokens) x 128 (features), 4 waves as 2 x 2, each 64 x 64 = 4 x 4
+// MFMA tiles of 16 x 16. Per pair of groups: the activation tile [128][128] goes through
+// LDS (shared by the two waves of a row band); each wave loads its four feature tiles'
+// packed codes (one 16-byte load per lane each) straight into B operands, turns them
+// into exact fp16 codes in registers, and two MFMA steps per group give each tile's
+// partial product; then acc += s * part + b * gsum.
+struct GemmArgs {
+  const _Float16 *x;
+  const u32x4 *codes;
+  const u32x4 *sb;
+  const float *gsT;  // [G][m_pad]
+  float *y;
+  int x_stride, M, K, N, y_stride, m_pad;
+};
+
+constexpr int kBM = 128, kBN = 128, kLdsRow = 128 + 8;
+
+template <int SD, bool ACC>
+__global__ __launch_bounds__(256) void gemm_q4a_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[kBM * kLdsRow];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, j4 = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  const int G = a.K / kGroup, G4 = quads_of(a.K), GP = 2 * G4;
+  const int T = tiles_of(a.N);
+
+  int tile[4];
+  bool tval[4];
+#pragma unroll
+  for (int ft = 0; ft < 4; ++ft) {
+    tile[ft] = (n0 >> 4) + wn * 4 + ft;
+    tval[ft] = tile[ft] < T;
+  }
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{};
+
+  for (int p = 0; p < (G + 1) / 2; ++p) {
+    // activation tile [128][128] (groups 2p, 2p+1) -> LDS: 2048 chunks of 8 halves, 8 per thread
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int chunk = tid + 256 * c;
+      const int r = chunk >> 4, kc = chunk & 15;
+      const int m = m0 + r, k = 128 * p + 8 * kc;
+      half8 v = {};
+      if (m < a.M && k < a.K) v = *reinterpret_cast<const half8 *>(a.x + (size_t)m * a.x_stride + k);
+      *reinterpret_cast<half8 *>(As + r * kLdsRow + 8 * kc) = v;
+    }
+    u32x4 wq[4], sq[4];
+#pragma unroll
+    for (int ft = 0; ft < 4; ++ft) {
+      wq[ft] = tval[ft] ? a.codes[((size_t)tile[ft] * GP + p) * 64 + lane] : u32x4{};
+      sq[ft] = tval[ft] ? a.sb[((size_t)tile[ft] * G4 + (p >> 1)) * 16 + c16] : u32x4{};
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      const int g = 2 * p + gg;
+      if (g >= G) break;
+      half8 bf[4][2];
+#pragma unroll
+      for (int ft = 0; ft < 4; ++ft)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) bf[ft][s] = nib8_to_half8(wq[ft][2 * gg + s]);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        half8 af[2];
+        const _Float16 *arow = As + (wm * 64 + mt * 16 + c16) * kLdsRow + 64 * gg + 8 * j4;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(arow + 32 * s);
+        const f32x4 gq = *reinterpret_cast<const f32x4 *>(a.gsT + (size_t)g * a.m_pad + m0 + wm * 64 + mt * 16 + 4 * j4);
+#pragma unroll
+        for (int ft = 0; ft < 4; ++ft) {
+          f32x4 pp = {};
+#pragma unroll
+          for (int s = 0; s < 2; ++s) pp = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bf[ft][s], pp, 0, 0, 0);
+          const uint32_t pr = sq[ft][2 * (p & 1) + gg];
+          const float sc = scale_f32<SD>((uint16_t)(pr & 0xFFFFu)) * kTwo24;
+          const float bi = scale_f32<SD>((uint16_t)(pr >> 16));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mt][ft][r] += sc * pp[r] + bi * gq[r];
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int ft = 0; ft < 4; ++ft) {
+      const int n = 16 * tile[ft] + c16;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * 64 + mt * 16 + 4 * j4 + r;
+        if (m < a.M) {
+          float *dst = a.y + (size_t)m * a.y_stride + n;
+          *dst = ACC ? *dst + acc[mt][ft][r] : acc[mt][ft][r];
+        }
+      }
+    }
+}
+
+static size_t gemm_workspace(int M, int K) {
+  const int m_pad = (M + kBM - 1) / kBM * kBM;
+  return kCounterBytes + (size_t)(K / kGroup) * m_pad * sizeof(float);
+}
+
+static int run_gemm(const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd, float *y,
+                    int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st) {
+  const size_t need = gemm_workspace(M, K);
+  RLQ_REQUIRE(ws_bytes >= need, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
+  RLQ_REQUIRE(aligned(ws, 16), "workspace must be 16-byte aligned");
+  const int m_pad = (M + kBM - 1) / kBM * kBM;
+  float *gsT = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterBytes);
+  // rows M..m_pad of gsT only feed output rows that are never stored
+  const int G = K / kGroup;
+  group_sums_kernel<<<(M * G + 255) / 256, 256, 0, st>>>(x, x_stride, M, K, nullptr, gsT, m_pad);
+  RLQ_HIP(hipGetLastError());
+  GemmArgs a;
+  a.x = x;
+  a.codes = static_cast<const u32x4 *>(packed);
+  a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
+  a.gsT = gsT; a.y = y;
+  a.x_stride = x_stride; a.M = M; a.K = K; a.N = N; a.y_stride = y_stride; a.m_pad = m_pad;
+  const dim3 grid((N + kBN - 1) / kBN, m_pad / kBM);
+  if (sd == RLQ_F16) {
+    if (accum) gemm_q4a_kernel<0, true><<<grid, 256, 0, st>>>(a);
+    else gemm_q4a_kernel<0, false><<<grid, 256, 0, st>>>(a);
+  } else {
+    if (accum) gemm_q4a_kernel<1, true><<<grid, 256, 0, st>>>(a);
+    else gemm_q4a_kernel<1, false><<<grid, 256, 0, st>>>(a);
+  }
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+static int check_linear_args(const char *fn, const void *x, int x_stride, int M, int K, int N, const void *packed,
+                             int sd, const float *y, int y_stride) {
   RLQ_REQUIRE(M >= 1 && N >= 1 && K >= kGroup, "%s: bad sizes M=%d K=%d N=%d", fn, M, K, N);
-  RLQ_REQUIRE(N <= 32 * kMaxTiles, "%s: N=%d exceeds the supported %d", fn, N, 32 * kMaxTiles);
   RLQ_REQUIRE(K % kGroup == 0, "%s: K=%d is not a multiple of the group size 64", fn, K);
+  RLQ_REQUIRE(N <= 16 * kMaxTiles, "%s: N=%d exceeds the supported %d", fn, N, 16 * kMaxTiles);
   RLQ_REQUIRE(sd == RLQ_F16 || sd == RLQ_BF16, "%s: unknown scale dtype %d", fn, sd);
-  RLQ_REQUIRE(x && w && s && b && y, "%s: null pointer argument", fn);
+  RLQ_REQUIRE(x && packed && y, "%s: null pointer argument", fn);
   RLQ_REQUIRE(x_stride >= K && x_stride % 8 == 0, "%s: x_stride=%d must be >= K and a multiple of 8", fn, x_stride);
   RLQ_REQUIRE(y_stride >= N, "%s: y_stride=%d < N=%d", fn, y_stride, N);
-  RLQ_REQUIRE(aligned(x, 16) && aligned(w, 16), "%s: x and w must be 16-byte aligned", fn);
-  RLQ_REQUIRE(aligned(s, 2) && aligned(b, 2) && aligned(y, 4), "%s: misaligned s, b or y", fn);
+  RLQ_REQUIRE(aligned(x, 16) && aligned(packed, 16), "%s: x and the packed weight must be 16-byte aligned", fn);
+  RLQ_REQUIRE(aligned(y, 4), "%s: misaligned y", fn);
   return 0;
 }
 
@@ -496,31 +660,64 @@ using namespace rlq;
 
 extern "C" {
 
+size_t rlq_packed_affine_bytes(int K, int N) {
+  if (K <= 0 || N <= 0 || K % kGroup) return 0;
+  return packed_bytes(K, N);
+}
+
+int rlq_pack_affine(const uint32_t *w, const void *s, const void *b, int K, int N, void *packed, void *stream) {
+  RLQ_REQUIRE(N >= 1 && K >= kGroup && K % kGroup == 0, "rlq_pack_affine: bad sizes K=%d N=%d", K, N);
+  RLQ_REQUIRE(w && s && b && packed, "rlq_pack_affine: null pointer argument");
+  RLQ_REQUIRE(aligned(w, 4) && aligned(packed, 16), "rlq_pack_affine: misaligned w or packed");
+  RLQ_REQUIRE(aligned(s, 2) && aligned(b, 2), "rlq_pack_affine: misaligned scales or biases");
+  const size_t pieces = (size_t)tiles_of(N) * 2 * quads_of(K) * 64;
+  auto codes = static_cast<u32x4 *>(packed);
+  auto sb = reinterpret_cast<u32x4 *>(static_cast<char *>(packed) + packed_code_bytes(K, N));
+  pack_mlx_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      w, static_cast<const uint16_t *>(s), static_cast<const uint16_t *>(b), K, N, codes, sb);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+int rlq_pack_affine_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const uint16_t *b_blk, int K, int n_pad,
+                            int row0, int rows, void *packed, void *stream) {
+  RLQ_REQUIRE(K >= kGroup && K % kGroup == 0, "rlq_pack_affine_blocked: K=%d is not a multiple of 64", K);
+  RLQ_REQUIRE(n_pad % 256 == 0 && n_pad > 0, "rlq_pack_affine_blocked: n_pad=%d is not a multiple of the block 256",
+              n_pad);
+  RLQ_REQUIRE(row0 >= 0 && rows >= 1 && row0 + rows <= n_pad, "rlq_pack_affine_blocked: rows [%d, %d) outside [0, %d)",
+              row0, row0 + rows, n_pad);
+  RLQ_REQUIRE(w_blk && s_blk && b_blk && packed, "rlq_pack_affine_blocked: null pointer argument");
+  RLQ_REQUIRE(aligned(packed, 16), "rlq_pack_affine_blocked: packed must be 16-byte aligned");
+  const size_t pieces = (size_t)tiles_of(rows) * 2 * quads_of(K) * 64;
+  auto codes = static_cast<u32x4 *>(packed);
+  auto sb = reinterpret_cast<u32x4 *>(static_cast<char *>(packed) + packed_code_bytes(K, rows));
+  pack_blocked_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      w_blk, s_blk, b_blk, K, row0, rows, codes, sb);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
 size_t rlq_linear_workspace_bytes(int M, int K, int N) {
   if (M <= 0 || K <= 0 || N <= 0 || K % kGroup) return 0;
-  return std::max(M <= 32 ? gemv_workspace(M, K, N) : (size_t)0, gemm_workspace(M, K));
+  return std::max(M <= kGemvMaxM ? gemv_workspace(M, K, N) : (size_t)0, gemm_workspace(M, K));
 }
 
-int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int K, int N, const uint32_t *w,
-                             const void *s, const void *b, int scale_dtype, float *y, int y_stride, int accum,
-                             void *workspace, size_t workspace_bytes, void *stream) {
-  int rc = check_linear_args("rlq_linear_affine", x, x_stride, M, K, N, w, s, b, scale_dtype, y, y_stride);
+int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int K, int N, const void *packed,
+                             int scale_dtype, float *y, int y_stride, int accum, void *workspace,
+                             size_t workspace_bytes, void *stream) {
+  int rc = check_linear_args("rlq_linear_affine", x, x_stride, M, K, N, packed, scale_dtype, y, y_stride);
   if (rc) return rc;
   RLQ_REQUIRE(kernel >= 0 && kernel <= 2, "rlq_linear_affine_kernel: unknown kernel %d", kernel);
-  const bool gemv = kernel == 1 || (kernel == 0 && M <= 32);
+  const bool gemv = kernel == 1 || (kernel == 0 && M <= kGemvMaxM);
   auto st = static_cast<hipStream_t>(stream);
   auto xh = static_cast<const _Float16 *>(x);
-  auto sh = static_cast<const uint16_t *>(s);
-  auto bh = static_cast<const uint16_t *>(b);
-  if (gemv)
-    return run_gemv(xh, x_stride, M, K, N, w, sh, bh, scale_dtype, y, y_stride, accum, workspace, workspace_bytes, st);
-  return run_gemm(xh, x_stride, M, K, N, w, sh, bh, scale_dtype, y, y_stride, accum, workspace, workspace_bytes, st);
+  if (gemv) return run_gemv(xh, x_stride, M, K, N, packed, scale_dtype, y, y_stride, accum, workspace, workspace_bytes, st);
+  return run_gemm(xh, x_stride, M, K, N, packed, scale_dtype, y, y_stride, accum, workspace, workspace_bytes, st);
 }
 
-int rlq_linear_affine(const void *x, int x_stride, int M, int K, int N, const uint32_t *w, const void *s,
-                      const void *b, int scale_dtype, float *y, int y_stride, int accum, void *workspace,
-                      size_t workspace_bytes, void *stream) {
-  return rlq_linear_affine_kernel(0, x, x_stride, M, K, N, w, s, b, scale_dtype, y, y_stride, accum, workspace,
+int rlq_linear_affine(const void *x, int x_stride, int M, int K, int N, const void *packed, int scale_dtype, float *y,
+                      int y_stride, int accum, void *workspace, size_t workspace_bytes, void *stream) {
+  return rlq_linear_affine_kernel(0, x, x_stride, M, K, N, packed, scale_dtype, y, y_stride, accum, workspace,
                                   workspace_bytes, stream);
 }
 
@@ -535,19 +732,19 @@ int rlq_group_sums(const void *x, int x_stride, int M, int K, float *gsum, void 
   return 0;
 }
 
-int rlq_dequant_affine(const uint32_t *w, const void *s, const void *b, int scale_dtype, int K, int N, float *out,
-                       void *stream) {
+int rlq_dequant_affine(const void *packed, int scale_dtype, int K, int N, float *out, void *stream) {
   RLQ_REQUIRE(N >= 1 && K >= kGroup && K % kGroup == 0, "rlq_dequant_affine: bad sizes K=%d N=%d", K, N);
-  RLQ_REQUIRE(w && s && b && out, "rlq_dequant_affine: null pointer argument");
+  RLQ_REQUIRE(packed && out, "rlq_dequant_affine: null pointer argument");
   RLQ_REQUIRE(scale_dtype == RLQ_F16 || scale_dtype == RLQ_BF16, "rlq_dequant_affine: unknown scale dtype %d",
               scale_dtype);
-  const size_t words = (size_t)N * (K / 8);
-  const unsigned blocks = (unsigned)((words + 255) / 256);
+  RLQ_REQUIRE(aligned(packed, 16), "rlq_dequant_affine: packed must be 16-byte aligned");
+  const size_t pieces = (size_t)tiles_of(N) * 2 * quads_of(K) * 64;
+  const unsigned blocks = (unsigned)((pieces + 255) / 256);
   auto st = static_cast<hipStream_t>(stream);
-  if (scale_dtype == RLQ_F16)
-    dequant_kernel<0><<<blocks, 256, 0, st>>>(w, static_cast<const uint16_t *>(s), static_cast<const uint16_t *>(b), K, N, out);
-  else
-    dequant_kernel<1><<<blocks, 256, 0, st>>>(w, static_cast<const uint16_t *>(s), static_cast<const uint16_t *>(b), K, N, out);
+  auto codes = static_cast<const u32x4 *>(packed);
+  auto sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
+  if (scale_dtype == RLQ_F16) dequant_kernel<0><<<blocks, 256, 0, st>>>(codes, sb, K, N, out);
+  else dequant_kernel<1><<<blocks, 256, 0, st>>>(codes, sb, K, N, out);
   RLQ_HIP(hipGetLastError());
   return 0;
 }
@@ -563,8 +760,8 @@ int rlq_repack_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const uint16
   const size_t words = (size_t)rows * (K / 8);
   repack_w_kernel<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(w_blk, K, row0, rows, w);
   RLQ_HIP(hipGetLastError());
-  const size_t sb = (size_t)rows * (K / kGroup);
-  repack_sb_kernel<<<(unsigned)((sb + 255) / 256), 256, 0, st>>>(s_blk, b_blk, K / kGroup, row0, rows, s, b);
+  const size_t sbn = (size_t)rows * (K / kGroup);
+  repack_sb_kernel<<<(unsigned)((sbn + 255) / 256), 256, 0, st>>>(s_blk, b_blk, K / kGroup, row0, rows, s, b);
   RLQ_HIP(hipGetLastError());
   return 0;
 }

@@ -24,16 +24,20 @@ SIGNATURES = {
     "rlq_set_fatal": (c_int, [c_int]),
     "rlq_last_error": (c_char_p, []),
     "rlq_set_device": (c_int, [c_int]),
-    "rlq_linear_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
-    "rlq_workspace_clear": (c_int, [c_void_p, c_size_t, c_void_p]),
-    "rlq_linear_affine": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
-                                  c_void_p, c_int, c_int, c_void_p, c_size_t, c_void_p]),
-    "rlq_linear_affine_kernel": (c_int, [c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
-                                         c_int, c_void_p, c_int, c_int, c_void_p, c_size_t, c_void_p]),
-    "rlq_group_sums": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
-    "rlq_dequant_affine": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "rlq_packed_affine_bytes": (c_size_t, [c_int, c_int]),
+    "rlq_pack_affine": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "rlq_pack_affine_blocked": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
+                                        c_void_p]),
     "rlq_repack_blocked": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
                                    c_void_p, c_void_p]),
+    "rlq_linear_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "rlq_workspace_clear": (c_int, [c_void_p, c_size_t, c_void_p]),
+    "rlq_linear_affine": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int, c_int,
+                                  c_void_p, c_size_t, c_void_p]),
+    "rlq_linear_affine_kernel": (c_int, [c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p,
+                                         c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "rlq_group_sums": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "rlq_dequant_affine": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
 }
 
 

@@ -1,15 +1,20 @@
 """Torch-facing host layer over the C ABI: the quantized linear of raceline's engine.
 
 Mirrors what Engine::encode_linear does for one QTensor (src/engine.mm:832-906): pick
-the kernel for the row count, bind the activations, the weight's codes, scales and
-biases and the output, and run it with ACCUM for the residual writers. Tensors are
-torch CUDA tensors (HBM plumbing only); every computation runs in libraceline_amd.so.
+the kernel for the row count, bind the activations, the packed weight and the output,
+and run it with ACCUM for the residual writers. Tensors are torch CUDA tensors (HBM
+plumbing only); every computation runs in libraceline_amd.so.
+
+Weights arrive in one of the reference's layouts (the MLX u32 layout of the BASELINE
+configs and tools/convert.py:82-89, or the blocked q4a layout of .rlm files,
+tools/convert.py:92-117) and are packed once, on the device, into the layout the kernels
+stream (see include/rlq.h); the dequantized value of every weight is unchanged.
 """
 
 from __future__ import annotations
 
 import threading
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
@@ -18,6 +23,7 @@ from . import lib
 GROUP = 64
 F16, BF16 = 0, 1
 KERNEL_AUTO, KERNEL_GEMV, KERNEL_GEMM = 0, 1, 2
+GEMV_MAX_M = 8
 
 
 def _ptr(t) -> int:
@@ -37,50 +43,80 @@ def scale_code(dtype: torch.dtype) -> int:
     raise ValueError(f"scales must be float16 or bfloat16, not {dtype}")
 
 
+def packed_bytes(K: int, N: int) -> int:
+    return int(lib.load().rlq_packed_affine_bytes(K, N))
+
+
 @dataclass
-class AffineWeight:
-    """A 4-bit affine matrix in the MLX layout (tools/convert.py:82-89): codes int32
-    [N][K/8] (bit pattern of the uint32 words), scales and biases [N][K/64] in float16
-    or bfloat16. Like the reference's QTensor (src/model_file.h:44-55) it may carry
-    named parts of a row-stacked matrix."""
-    w: torch.Tensor
-    s: torch.Tensor
-    b: torch.Tensor
-    parts: dict | None = None
+class PackedWeight:
+    """A 4-bit affine matrix [N][K] in the packed device layout, with the dtype of its
+    16-bit scales and biases. Like the reference's QTensor (src/model_file.h:44-55) it
+    may name the row ranges of stacked parts."""
+    packed: torch.Tensor            # uint8, rlq_packed_affine_bytes(K, N) bytes
+    K: int
+    N: int
+    scale_dtype: torch.dtype = torch.float16
+    parts: dict = field(default_factory=dict)
 
     def __post_init__(self):
-        if self.w.dtype not in (torch.int32, torch.uint32):
-            raise TypeError("codes must be 32-bit words")
-        N, K8 = self.w.shape
-        if self.s.shape != (N, K8 * 8 // GROUP) or self.b.shape != self.s.shape:
-            raise ValueError(f"scales/biases {tuple(self.s.shape)} do not match codes {tuple(self.w.shape)}")
-        if self.s.dtype != self.b.dtype:
-            raise TypeError("scales and biases must share a dtype")
-        for t in (self.w, self.s, self.b):
-            if not t.is_contiguous():
-                raise ValueError("weight tensors must be contiguous")
+        if self.packed.dtype != torch.uint8 or not self.packed.is_contiguous():
+            raise TypeError("packed weight must be a contiguous uint8 tensor")
+        if self.packed.numel() < packed_bytes(self.K, self.N):
+            raise ValueError("packed buffer is smaller than the layout needs")
 
     @property
-    def N(self) -> int:
-        return self.w.shape[0]
+    def code(self) -> int:
+        return scale_code(self.scale_dtype)
 
-    @property
-    def K(self) -> int:
-        return self.w.shape[1] * 8
 
-    @property
-    def scale_dtype(self) -> int:
-        return scale_code(self.s.dtype)
+def _check_mlx(w: torch.Tensor, s: torch.Tensor, b: torch.Tensor):
+    if w.dtype not in (torch.int32, torch.uint32) or w.dim() != 2:
+        raise TypeError("codes must be 32-bit words [N][K/8]")
+    N, K8 = w.shape
+    if s.shape != (N, K8 * 8 // GROUP) or b.shape != s.shape:
+        raise ValueError(f"scales/biases {tuple(s.shape)} do not match codes {tuple(w.shape)}")
+    if s.dtype != b.dtype:
+        raise TypeError("scales and biases must share a dtype")
+    for t in (w, s, b):
+        if not t.is_contiguous():
+            raise ValueError("weight tensors must be contiguous")
+    return N, K8 * 8
 
-    def part(self, name: str) -> "AffineWeight":
-        off, n = self.parts[name]
-        return AffineWeight(self.w[off:off + n], self.s[off:off + n], self.b[off:off + n])
+
+def pack_affine(w: torch.Tensor, s: torch.Tensor, b: torch.Tensor, stream=None) -> PackedWeight:
+    """MLX layout (codes [N][K/8] 32-bit words, scales and biases [N][K/64]) -> PackedWeight."""
+    N, K = _check_mlx(w, s, b)
+    out = torch.empty(packed_bytes(K, N), dtype=torch.uint8, device=w.device)
+    lib.call("rlq_pack_affine", _ptr(w), _ptr(s), _ptr(b), K, N, _ptr(out), _stream(stream))
+    return PackedWeight(out, K, N, s.dtype)
+
+
+def pack_blocked(w_blk: torch.Tensor, s_blk: torch.Tensor, b_blk: torch.Tensor, K: int, n_pad: int, row0: int,
+                 rows: int, scale_dtype: torch.dtype = torch.bfloat16, stream=None) -> PackedWeight:
+    """Rows [row0, row0 + rows) of a blocked q4a tensor of a .rlm file (already in device
+    memory) -> PackedWeight."""
+    out = torch.empty(packed_bytes(K, rows), dtype=torch.uint8, device=w_blk.device)
+    lib.call("rlq_pack_affine_blocked", _ptr(w_blk), _ptr(s_blk), _ptr(b_blk), K, n_pad, row0, rows, _ptr(out),
+             _stream(stream))
+    return PackedWeight(out, K, rows, scale_dtype)
+
+
+def repack_blocked(w_blk: torch.Tensor, s_blk: torch.Tensor, b_blk: torch.Tensor, K: int, n_pad: int,
+                   row0: int, rows: int, scale_dtype: torch.dtype = torch.bfloat16, stream=None):
+    """Blocked q4a rows -> MLX layout tensors (w int32 [rows][K/8], s, b [rows][K/64])."""
+    dev = w_blk.device
+    w = torch.empty((rows, K // 8), dtype=torch.int32, device=dev)
+    s = torch.empty((rows, K // GROUP), dtype=scale_dtype, device=dev)
+    b = torch.empty((rows, K // GROUP), dtype=scale_dtype, device=dev)
+    lib.call("rlq_repack_blocked", _ptr(w_blk), _ptr(s_blk), _ptr(b_blk), K, n_pad, row0, rows, _ptr(w), _ptr(s),
+             _ptr(b), _stream(stream))
+    return w, s, b
 
 
 class _Workspaces:
-    """One zero-filled scratch buffer per device, grown on demand. Kernels leave it
-    zeroed, so it is cleared only when (re)allocated. Calls that use it must not
-    overlap on two streams of one device."""
+    """One zero-filled scratch buffer per device, grown on demand. Kernels leave its
+    counter area zeroed, so it is cleared only when (re)allocated. Calls that use it must
+    not overlap on two streams of one device."""
 
     def __init__(self):
         self._bufs = {}
@@ -105,12 +141,12 @@ def workspace_bytes(M: int, K: int, N: int) -> int:
     return int(lib.load().rlq_linear_workspace_bytes(M, K, N))
 
 
-def linear(x: torch.Tensor, wt: AffineWeight, out: torch.Tensor | None = None, accum: bool = False,
+def linear(x: torch.Tensor, pw: PackedWeight, out: torch.Tensor | None = None, accum: bool = False,
            kernel: int = KERNEL_AUTO, stream=None) -> torch.Tensor:
     """out[m][n] (+)= sum_k x[m][k] * W[n][k] for fp16 x [M][>=K] (row stride x.stride(0))."""
     if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("x must be a row-major float16 matrix")
-    M, K, N = x.shape[0], wt.K, wt.N
+    M, K, N = x.shape[0], pw.K, pw.N
     if x.shape[1] < K:
         raise ValueError(f"x has {x.shape[1]} columns, the weight needs {K}")
     if out is None:
@@ -121,8 +157,8 @@ def linear(x: torch.Tensor, wt: AffineWeight, out: torch.Tensor | None = None, a
         raise ValueError("out must be a row-major float32 [M][>=N] matrix")
     nbytes = workspace_bytes(M, K, N)
     ws = _WS.get(x.device, nbytes)
-    lib.call("rlq_linear_affine_kernel", kernel, _ptr(x), x.stride(0), M, K, N, _ptr(wt.w), _ptr(wt.s), _ptr(wt.b),
-             wt.scale_dtype, _ptr(out), out.stride(0), 1 if accum else 0, _ptr(ws), 0 if ws is None else ws.numel(),
+    lib.call("rlq_linear_affine_kernel", kernel, _ptr(x), x.stride(0), M, K, N, _ptr(pw.packed), pw.code,
+             _ptr(out), out.stride(0), 1 if accum else 0, _ptr(ws), 0 if ws is None else ws.numel(),
              _stream(stream))
     return out
 
@@ -134,21 +170,7 @@ def group_sums(x: torch.Tensor, K: int | None = None, stream=None) -> torch.Tens
     return out
 
 
-def dequant(wt: AffineWeight, stream=None) -> torch.Tensor:
-    out = torch.empty((wt.N, wt.K), dtype=torch.float32, device=wt.w.device)
-    lib.call("rlq_dequant_affine", _ptr(wt.w), _ptr(wt.s), _ptr(wt.b), wt.scale_dtype, wt.K, wt.N, _ptr(out),
-             _stream(stream))
+def dequant(pw: PackedWeight, stream=None) -> torch.Tensor:
+    out = torch.empty((pw.N, pw.K), dtype=torch.float32, device=pw.packed.device)
+    lib.call("rlq_dequant_affine", _ptr(pw.packed), pw.code, pw.K, pw.N, _ptr(out), _stream(stream))
     return out
-
-
-def repack_blocked(w_blk: torch.Tensor, s_blk: torch.Tensor, b_blk: torch.Tensor, K: int, n_pad: int,
-                   row0: int, rows: int, scale_dtype: torch.dtype = torch.bfloat16, stream=None) -> AffineWeight:
-    """Blocked q4a tensor of a .rlm file (already in device memory) -> AffineWeight for
-    rows [row0, row0 + rows)."""
-    dev = w_blk.device
-    w = torch.empty((rows, K // 8), dtype=torch.int32, device=dev)
-    s = torch.empty((rows, K // GROUP), dtype=scale_dtype, device=dev)
-    b = torch.empty((rows, K // GROUP), dtype=scale_dtype, device=dev)
-    lib.call("rlq_repack_blocked", _ptr(w_blk), _ptr(s_blk), _ptr(b_blk), K, n_pad, row0, rows, _ptr(w), _ptr(s),
-             _ptr(b), _stream(stream))
-    return AffineWeight(w, s, b)

@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import torch
 
-from .ops import GROUP, AffineWeight
+from .ops import GROUP, pack_affine
 
 
 def pack_codes(q: torch.Tensor) -> torch.Tensor:
@@ -28,7 +28,8 @@ def pack_codes(q: torch.Tensor) -> torch.Tensor:
     return words.to(torch.int32).contiguous()
 
 
-def quantize_affine(W: torch.Tensor, scale_dtype: torch.dtype = torch.float16) -> AffineWeight:
+def quantize_affine(W: torch.Tensor, scale_dtype: torch.dtype = torch.float16):
+    """[N][K] float weights -> MLX layout (codes int32 [N][K/8], scales, biases [N][K/64])."""
     W = W.to(torch.float32)
     N, K = W.shape
     g = W.view(N, K // GROUP, GROUP)
@@ -41,24 +42,28 @@ def quantize_affine(W: torch.Tensor, scale_dtype: torch.dtype = torch.float16) -
     bf = b.float().unsqueeze(-1)
     q = torch.clamp(torch.round((g - bf) / sf), 0, 15)
     q = torch.where(sf == 0, torch.zeros_like(q), q)
-    return AffineWeight(pack_codes(q.view(N, K)), s.contiguous(), b.contiguous())
+    return pack_codes(q.view(N, K)), s.contiguous(), b.contiguous()
 
 
 def random_affine(N: int, K: int, seed: int, device, std: float = 0.02,
-                  scale_dtype: torch.dtype = torch.float16, chunk_rows: int = 8192) -> AffineWeight:
-    """N(0, std) weights quantized per group; generated in row chunks to bound memory."""
+                  scale_dtype: torch.dtype = torch.float16, chunk_rows: int = 8192, packed: bool = True):
+    """N(0, std) weights quantized per group, generated in row chunks to bound memory.
+    Returns a PackedWeight, or the MLX-layout (w, s, b) tensors when packed is False."""
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     ws, ss, bs = [], [], []
     for r0 in range(0, N, chunk_rows):
         r = min(chunk_rows, N - r0)
         W = torch.randn((r, K), generator=gen, device=device, dtype=torch.float32) * std
-        a = quantize_affine(W, scale_dtype)
-        ws.append(a.w)
-        ss.append(a.s)
-        bs.append(a.b)
+        w, s, b = quantize_affine(W, scale_dtype)
+        ws.append(w)
+        ss.append(s)
+        bs.append(b)
         del W
-    return AffineWeight(torch.cat(ws), torch.cat(ss), torch.cat(bs))
+    mlx = (torch.cat(ws), torch.cat(ss), torch.cat(bs))
+    if not packed:
+        return mlx
+    return pack_affine(*mlx)
 
 
 def random_activations(M: int, K: int, seed: int, device, outliers: float = 0.0) -> torch.Tensor:

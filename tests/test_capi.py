@@ -27,7 +27,8 @@ def declared_functions():
 
 def test_header_declares_the_path():
     names = declared_functions()
-    for must in ("rlq_linear_affine", "rlq_dequant_affine", "rlq_repack_blocked", "rlq_group_sums"):
+    for must in ("rlq_linear_affine", "rlq_dequant_affine", "rlq_repack_blocked", "rlq_group_sums",
+                 "rlq_pack_affine", "rlq_pack_affine_blocked", "rlq_packed_affine_bytes"):
         assert must in names
 
 
@@ -46,23 +47,33 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_workspace_query():
     L = lib.load()
     assert L.rlq_abi_version() == 1
-    assert L.rlq_linear_workspace_bytes(1, 4096, 4096) > 0      # small N splits K over workgroups
+    assert L.rlq_linear_workspace_bytes(64, 4096, 4096) > 0     # the prefill kernel stages group sums
     assert L.rlq_linear_workspace_bytes(1, 100, 4096) == 0      # invalid K: nothing to size
-    # the split of K, hence the workspace per token row, does not depend on M
-    a = L.rlq_linear_workspace_bytes(1, 4096, 1024)
-    b = L.rlq_linear_workspace_bytes(8, 4096, 1024)
-    assert b > a
+    # packed layout: 2304 bytes per (16-row tile, quad of groups of 64)
+    assert L.rlq_packed_affine_bytes(4096, 4096) == 256 * 16 * 2304
+    assert L.rlq_packed_affine_bytes(64, 33) == 3 * 1 * 2304
+    assert L.rlq_linear_workspace_bytes(256, 4096, 1024) > L.rlq_linear_workspace_bytes(64, 4096, 1024)
 
 
 def test_bad_arguments_return_an_error_in_nonfatal_mode():
     with pytest.raises(lib.RlqError, match="multiple of the group size"):
-        lib.call("rlq_linear_affine", 16, 100, 1, 100, 10, 16, 16, 16, 0, 16, 10, 0, None, 0, None)
+        lib.call("rlq_linear_affine", 16, 100, 1, 100, 10, 16, 0, 16, 10, 0, None, 0, None)
     with pytest.raises(lib.RlqError, match="unknown scale dtype"):
-        lib.call("rlq_linear_affine", 16, 64, 1, 64, 10, 16, 16, 16, 7, 16, 10, 0, None, 0, None)
+        lib.call("rlq_linear_affine", 16, 64, 1, 64, 10, 16, 7, 16, 10, 0, None, 0, None)
     with pytest.raises(lib.RlqError, match="x_stride"):
-        lib.call("rlq_linear_affine", 16, 60, 1, 64, 10, 16, 16, 16, 0, 16, 10, 0, None, 0, None)
+        lib.call("rlq_linear_affine", 16, 60, 1, 64, 10, 16, 0, 16, 10, 0, None, 0, None)
     with pytest.raises(lib.RlqError, match="null pointer"):
-        lib.call("rlq_linear_affine", None, 64, 1, 64, 10, 16, 16, 16, 0, 16, 10, 0, None, 0, None)
+        lib.call("rlq_linear_affine", None, 64, 1, 64, 10, 16, 0, 16, 10, 0, None, 0, None)
+    with pytest.raises(lib.RlqError, match="16-byte aligned"):
+        lib.call("rlq_linear_affine", 8, 64, 1, 64, 10, 16, 0, 16, 10, 0, None, 0, None)
+    with pytest.raises(lib.RlqError, match="unknown kernel"):
+        lib.call("rlq_linear_affine_kernel", 5, 16, 64, 1, 64, 10, 16, 0, 16, 10, 0, None, 0, None)
+    with pytest.raises(lib.RlqError, match="decode kernel handles M <= 8"):
+        lib.call("rlq_linear_affine_kernel", 1, 16, 64, 9, 64, 10, 16, 0, 16, 10, 0, None, 0, None)
+    with pytest.raises(lib.RlqError, match="workspace"):
+        lib.call("rlq_linear_affine_kernel", 2, 16, 4096, 64, 4096, 1024, 16, 0, 16, 1024, 0, None, 0, None)
+    with pytest.raises(lib.RlqError, match="block 256"):
+        lib.call("rlq_pack_affine_blocked", 16, 16, 16, 64, 300, 0, 10, 16, None)
     with pytest.raises(lib.RlqError, match="block 256"):
         lib.call("rlq_repack_blocked", 16, 16, 16, 64, 300, 0, 10, 16, 16, 16, None)
     with pytest.raises(lib.RlqError, match="outside"):
@@ -73,8 +84,8 @@ def test_bad_arguments_return_an_error_in_nonfatal_mode():
 def test_errors_are_fatal_by_default():
     code = ("import ctypes, sys; sys.path.insert(0, %r); from raceline_amd import lib; "
             "L = ctypes.CDLL(lib.library_path()); "
-            "L.rlq_linear_affine(ctypes.c_void_p(16), 100, 1, 100, 10, ctypes.c_void_p(16), ctypes.c_void_p(16), "
-            "ctypes.c_void_p(16), 0, ctypes.c_void_p(16), 10, 0, None, ctypes.c_size_t(0), None); "
+            "L.rlq_linear_affine(ctypes.c_void_p(16), 100, 1, 100, 10, ctypes.c_void_p(16), 0, "
+            "ctypes.c_void_p(16), 10, 0, None, ctypes.c_size_t(0), None); "
             "print('not reached')") % ROOT
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert r.returncode == 1

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from tests.qdata import make_layer, make_x, sample_cols, to_dev, upload
+from tests.qdata import make_layer, make_x, packed_layout_np, to_dev, upload, upload_mlx
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -55,9 +55,9 @@ def test_dequant_bit_exact(gpu, sd):
     assert same.all(), f"{(~same).sum()} dequantized weights differ"
 
 
-GEMV_CASES = [  # (M, K, N)
+GEMV_CASES = [  # (M, K, N); the decode kernel takes M <= 8
     (1, 256, 32), (1, 4096, 4096), (5, 2560, 9216), (3, 9216, 2560), (2, 2560, 1000),
-    (8, 512, 2048), (16, 1024, 300), (32, 2048, 1024), (17, 640, 96), (1, 17408, 640), (4, 64, 33),
+    (8, 512, 2048), (8, 1024, 300), (7, 640, 96), (1, 17408, 640), (4, 64, 33), (1, 12288, 4096),
 ]
 
 
@@ -71,7 +71,7 @@ def test_gemv_parity(gpu, M, K, N):
     O.check_close(y[:, :N], ref, TOL, f"gemv M={M} K={K} N={N}")
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (7, 4096, 1024), (32, 512, 96)])
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (7, 4096, 1024), (8, 512, 96)])
 def test_gemv_accumulates(gpu, M, K, N):
     q, s, b = make_layer(7, N, K)
     x = make_x(8, M, K)
@@ -81,8 +81,8 @@ def test_gemv_accumulates(gpu, M, K, N):
     O.check_close(y, ref, TOL, "gemv accum")
 
 
-GEMM_CASES = [(33, 256, 64), (130, 5120, 1024), (512, 2048, 1024), (70, 9216, 2560), (256, 1024, 300),
-              (40, 2560, 1000)]
+GEMM_CASES = [(9, 512, 96), (16, 1024, 300), (32, 2048, 1024), (33, 256, 64), (130, 5120, 1024),
+              (512, 2048, 1024), (70, 9216, 2560), (256, 1024, 300), (40, 2560, 1000)]
 
 
 @pytest.mark.parametrize("M,K,N", GEMM_CASES)
@@ -130,6 +130,7 @@ def test_repeat_calls_reuse_workspace(gpu):
 
 @pytest.mark.parametrize("sd", ["f16", "bf16"])
 def test_repack_blocked_round_trip(gpu, sd):
+    """.rlm blocked q4a tensor (tools/convert.py:92-117) -> MLX layout, per stacked part."""
     import torch
 
     from raceline_amd import ops
@@ -140,11 +141,52 @@ def test_repack_blocked_round_trip(gpu, sd):
     wb, sb, bb = to_dev(w, gpu), to_dev(s.view(np.int16), gpu), to_dev(b.view(np.int16), gpu)
     dt = torch.float16 if sd == "f16" else torch.bfloat16
     for (off, rows), (q, s_p, b_p) in zip(offs, parts):
-        wt = ops.repack_blocked(wb, sb, bb, K, n_pad, off, rows, scale_dtype=dt)
+        wt, st, bt = ops.repack_blocked(wb, sb, bb, K, n_pad, off, rows, scale_dtype=dt)
         torch.cuda.synchronize()
-        np.testing.assert_array_equal(wt.w.cpu().numpy().view(np.uint32), O.pack_nibbles_u32(q))
-        np.testing.assert_array_equal(wt.s.cpu().view(torch.int16).numpy().view(np.uint16), s_p)
-        np.testing.assert_array_equal(wt.b.cpu().view(torch.int16).numpy().view(np.uint16), b_p)
+        np.testing.assert_array_equal(wt.cpu().numpy().view(np.uint32), O.pack_nibbles_u32(q))
+        np.testing.assert_array_equal(st.cpu().view(torch.int16).numpy().view(np.uint16), s_p)
+        np.testing.assert_array_equal(bt.cpu().view(torch.int16).numpy().view(np.uint16), b_p)
+
+
+@pytest.mark.parametrize("sd", ["f16", "bf16"])
+def test_packed_layout(gpu, sd):
+    """The upload packers (from the MLX layout and from the blocked file layout) both
+    produce exactly the layout include/rlq.h documents."""
+    import torch
+
+    from raceline_amd import ops
+
+    K = 320
+    parts = [make_layer(40 + i, rows, K, sd) for i, rows in enumerate((70, 33))]
+    for q, s_p, b_p in parts:
+        pw = upload(q, s_p, b_p, sd, gpu)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(pw.packed.cpu().numpy(), packed_layout_np(q, s_p, b_p))
+    w, s, b, n_pad, offs = O.pack_blocked(parts)
+    wb, sb, bb = to_dev(w, gpu), to_dev(s.view(np.int16), gpu), to_dev(b.view(np.int16), gpu)
+    dt = torch.float16 if sd == "f16" else torch.bfloat16
+    for (off, rows), (q, s_p, b_p) in zip(offs, parts):
+        pw = ops.pack_blocked(wb, sb, bb, K, n_pad, off, rows, scale_dtype=dt)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(pw.packed.cpu().numpy(), packed_layout_np(q, s_p, b_p))
+
+
+def test_blocked_file_tensor_end_to_end(gpu):
+    """A stacked q/k/v tensor in the .rlm blocked layout with bf16 scales (what
+    tools/convert.py writes): pack each part on the device and run the decode kernel."""
+    import torch
+
+    from raceline_amd import ops
+
+    K = 1024
+    parts = [make_layer(50 + i, rows, K, "bf16") for i, rows in enumerate((512, 128, 128))]
+    w, s, b, n_pad, offs = O.pack_blocked(parts)
+    wb, sb, bb = to_dev(w, gpu), to_dev(s.view(np.int16), gpu), to_dev(b.view(np.int16), gpu)
+    x = make_x(51, 3, K)
+    for (off, rows), (q, s_p, b_p) in zip(offs, parts):
+        pw = ops.pack_blocked(wb, sb, bb, K, n_pad, off, rows, scale_dtype=torch.bfloat16)
+        y = _run(gpu, x, pw, kernel=1)
+        O.check_close(y, O.linear_affine_f64(x, q, s_p, b_p, "bf16"), TOL, f"blocked part at {off}")
 
 
 def test_group_sums(gpu):

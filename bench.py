@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the 4-bit quantized matmul path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu] [--profile]
 
 Headline (BASELINE metric "4-bit GEMV achieved HBM GB/s at M=1"): one step is the
 9B-class decode layer's six projections (q, k, v, o, gate_up, down)
@@ -206,6 +206,53 @@ def cpu_baseline(device, budget_s=15.0):
     }
 
 
+PROFILE_TRAFFIC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "gemv_q4a_9b_gate_up_m1_traffic.txt")
+CALIBRATION_BYTES = 256 << 20  # the elementwise calibration kernel reads and writes this much
+
+
+def profile_dominant(launches):
+    """--profile: the dominant kernel alone (9B gate_up at M=1), launched eagerly over its
+    rotating weight copies, then a plain elementwise kernel of known traffic (torch.neg
+    over 256 MiB of float32: reads 256 MiB, writes 256 MiB) that calibrates rocprofv3's
+    FETCH_SIZE and WRITE_SIZE counters. Meant to run under rocprofv3."""
+    import torch
+
+    from raceline_amd import lib, ops, synth
+    from raceline_amd.configs import CFG2_9B
+
+    lib.load()
+    dev = torch.device("cuda:0")
+    _, K, N = [c for c in CFG2_9B if c[0] == "gate_up"][0]
+    shapes = [("gate_up", K, N)]
+    copies = copies_for(shapes)
+    ws = [synth.random_affine(N, K, 1 + 1000 * c, dev) for c in range(copies)]
+    x = synth.random_activations(1, K, 99, dev)
+    y = torch.empty((1, N), dtype=torch.float32, device=dev)
+    for i in range(launches):
+        ops.linear(x, ws[i % copies], out=y)
+    torch.cuda.synchronize()
+    a = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(10):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    log(f"[profile] gemv_q4a K={K} N={N} M=1: {launches} launches over {copies} copies; "
+        f"calibration: 10 x torch.neg over {CALIBRATION_BYTES >> 20} MiB")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration kernel), or None."""
+    try:
+        for line in open(PROFILE_TRAFFIC):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(float(line.split("=")[1]))
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -213,6 +260,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail configs, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="launch only the dominant kernel and a calibration kernel (for rocprofv3)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -220,6 +269,10 @@ def main():
         print("bench.py measures one GPU: this build's path runs on a single MI355X (the multi-GPU "
               "sharding is a design only); run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.profile:
+        profile_dominant(max(args.steps, 40))
+        return
 
     import torch
 
@@ -248,7 +301,7 @@ def main():
     t_gu = time_kernel(l9, CFG2_9B, 1, gu, dev, launches=4 * copies)
     ach = linear_bytes(1, Kg, Ng) / t_gu / 1e9
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                 "kernel": "gemv_q4a_kernel<1,16,0,false> (9B gate_up, M=1, K=4096, N=24576)",
                 "avg_launch_us": round(t_gu * 1e6, 2), "algorithmic_bytes": linear_bytes(1, Kg, Ng)}
 

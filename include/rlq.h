@@ -77,10 +77,10 @@ int rlq_repack_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const uint16
 
 /* ---------------------------------------------------------------- dense affine linear */
 
-/* Bytes of scratch rlq_linear_affine needs for these sizes. The scratch must be zero-filled
- * once when it is allocated (rlq_workspace_clear); calls leave its counter area zeroed. */
+/* Bytes of scratch rlq_linear_affine needs for these sizes (0 for the decode kernel; the
+ * prefill kernel stages the activations' group sums there). Contents need no initialisation
+ * and are not kept between calls; calls that share one workspace must not overlap. */
 size_t rlq_linear_workspace_bytes(int M, int K, int N);
-int rlq_workspace_clear(void *workspace, size_t bytes, void *stream);
 
 /* y[m][n] = sum_k x[m][k] * W[n][k]   (accum = 0)
  * y[m][n] += that                      (accum = 1: the residual add, ACCUM in the reference)

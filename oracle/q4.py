@@ -25,7 +25,7 @@ __all__ = [
     "quantize_affine_rtn", "dequant_affine", "dequant_native",
     "group_sums", "linear_affine_f64", "linear_affine_factored_f64", "linear_affine_cpu_f32",
     "linear_native_f64", "check_close", "rel_err",
-    "XorShift64",
+    "XorShift64", "reference_test_case", "REFERENCE_TEST_CASES",
 ]
 
 
@@ -369,6 +369,92 @@ class XorShift64:
 
     def codes(self, count: int) -> np.ndarray:
         return np.array([self.next() & 15 for _ in range(count)], dtype=np.uint8)
+
+    # xorshift64 is linear over GF(2): one step is a 64x64 bit matrix T, so the state L steps
+    # ahead is T^L applied to the current one. stream() computes L outputs serially, then
+    # every later block of L as T^L of the previous block, with T^L applied through eight
+    # byte-indexed tables (out = XOR_p table[p][byte p of the state]).
+    _BLOCK = 1 << 16
+    _tables = None
+
+    @staticmethod
+    def _step(s: int) -> int:
+        m = XorShift64.MASK
+        s ^= (s << 13) & m
+        s ^= s >> 7
+        s ^= (s << 17) & m
+        return s
+
+    @classmethod
+    def _jump_tables(cls) -> np.ndarray:
+        if cls._tables is None:
+            def apply(cols, v):
+                r = 0
+                for i in range(64):
+                    if (v >> i) & 1:
+                        r ^= cols[i]
+                return r
+            cols = [cls._step(1 << c) for c in range(64)]                 # columns of T
+            for _ in range(cls._BLOCK.bit_length() - 1):                  # T^(2^k), k -> log2(BLOCK)
+                cols = [apply(cols, cols[c]) for c in range(64)]
+            t = np.zeros((8, 256), dtype=np.uint64)
+            for p in range(8):
+                for v in range(256):
+                    t[p, v] = np.uint64(apply(cols[8 * p:8 * p + 8] + [0] * 56, v))
+            cls._tables = t
+        return cls._tables
+
+    def stream(self, count: int) -> np.ndarray:
+        """The next `count` outputs as uint64, identical to `count` calls of next()."""
+        L = self._BLOCK
+        first = min(count, L)
+        out = np.empty(count, dtype=np.uint64)
+        for i in range(first):
+            out[i] = self.next()
+        if count > L:
+            t = self._jump_tables()
+            for b0 in range(L, count, L):
+                prev = out[b0 - L:b0]
+                nxt = t[0][(prev & np.uint64(0xFF)).astype(np.intp)]
+                for p in range(1, 8):
+                    nxt = nxt ^ t[p][((prev >> np.uint64(8 * p)) & np.uint64(0xFF)).astype(np.intp)]
+                n = min(L, count - b0)
+                out[b0:b0 + n] = nxt[:n]
+            self.state = int(out[-1])
+        return out
+
+    @staticmethod
+    def uniform_of(r: np.ndarray, lo: float, hi: float) -> np.ndarray:
+        """uniform(lo, hi) of tests/test_linear.mm:39 for each output r (vectorised):
+        lo + (hi - lo) * float((r >> 11) * 2^-53), the last two operations in float32."""
+        u = ((np.asarray(r, dtype=np.uint64) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0))
+        return np.float32(lo) + (np.float32(hi) - np.float32(lo)) * u.astype(np.float32)
+
+
+def reference_test_case(M: int, K: int, N: int, gen: XorShift64 | None = None):
+    """The inputs of one correctness case of tests/test_linear.mm (check(), :149-185), drawn
+    as make_layer(keep_ref) (:68-89) and make_input (:141-147) draw them:
+    codes rnd() & 15 row-major [N][K]; per (row, group) s = bf16(U(0.001, 0.012)) then
+    b = bf16(-7.5 s + U(-0.01, 0.01)); activations fp16(U(-2, 2)) [M][K].
+    Each case starts from the test's seed. (The reference's compiler may contract
+    -7.5*s + u into one fused multiply-add; that can move a bias by one bf16 step, which
+    does not matter here because parity is computed from the stored values.)
+    Returns (q uint8 [N][K], s, b uint16 bf16 bits [N][K/64], x float16 [M][K])."""
+    gen = gen or XorShift64()
+    G = K // GROUP
+    q = (gen.stream(N * K) & np.uint64(15)).astype(np.uint8).reshape(N, K)
+    r = gen.stream(2 * N * G)
+    sv = XorShift64.uniform_of(r[0::2], 0.001, 0.012)
+    s = f32_to_bf16_bits(sv)
+    bv = np.float32(-7.5) * sv + XorShift64.uniform_of(r[1::2], -0.01, 0.01)
+    b = f32_to_bf16_bits(bv.astype(np.float32))
+    x = XorShift64.uniform_of(gen.stream(M * K), -2.0, 2.0).astype(np.float16).reshape(M, K)
+    return q, s.reshape(N, G), b.reshape(N, G), x
+
+
+# The correctness cases of tests/test_linear.mm:440-446 as (M, K, N).
+REFERENCE_TEST_CASES = [(1, 2560, 9216), (5, 2560, 9216), (40, 2560, 9216), (70, 2560, 9216),
+                        (3, 9216, 2560), (2, 2560, 1000), (130, 5120, 1024)]
 
 
 PINNED_BY = {

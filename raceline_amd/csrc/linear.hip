@@ -37,10 +37,7 @@ namespace rlq {
 
 constexpr int kGroup = 64;
 
-// Workspace layout: a fixed area of counters first (kept zero between calls, so it must
-// not move with the shape of a call), then the per-call scratch (group sums).
 constexpr int kMaxTiles = 32768;                                   // N <= 16 * kMaxTiles
-constexpr size_t kCounterBytes = 65536;
 
 __host__ __device__ inline int tiles_of(int N) { return (N + 15) / 16; }
 __host__ __device__ inline int quads_of(int K) { return (K / kGroup + 3) / 4; }
@@ -608,7 +605,7 @@ __global__ __launch_bounds__(256) void gemm_q4a_kernel(GemmArgs a) {
 
 static size_t gemm_workspace(int M, int K) {
   const int m_pad = (M + kBM - 1) / kBM * kBM;
-  return kCounterBytes + (size_t)(K / kGroup) * m_pad * sizeof(float);
+  return (size_t)(K / kGroup) * m_pad * sizeof(float);   // group sums, transposed
 }
 
 static int run_gemm(const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd, float *y,
@@ -617,7 +614,7 @@ static int run_gemm(const _Float16 *x, int x_stride, int M, int K, int N, const 
   RLQ_REQUIRE(ws_bytes >= need, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
   RLQ_REQUIRE(aligned(ws, 16), "workspace must be 16-byte aligned");
   const int m_pad = (M + kBM - 1) / kBM * kBM;
-  float *gsT = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterBytes);
+  float *gsT = static_cast<float *>(ws);
   // rows M..m_pad of gsT only feed output rows that are never stored
   const int G = K / kGroup;
   group_sums_kernel<<<(M * G + 255) / 256, 256, 0, st>>>(x, x_stride, M, K, nullptr, gsT, m_pad);

@@ -50,11 +50,5 @@ int rlq_set_device(int device) {
   return 0;
 }
 
-int rlq_workspace_clear(void *workspace, size_t bytes, void *stream) {
-  if (bytes == 0) return 0;
-  RLQ_REQUIRE(workspace != nullptr, "rlq_workspace_clear: null workspace of %zu bytes", bytes);
-  RLQ_HIP(hipMemsetAsync(workspace, 0, bytes, static_cast<hipStream_t>(stream)));
-  return 0;
-}
 
 }  // extern "C"

@@ -31,7 +31,6 @@ SIGNATURES = {
     "rlq_repack_blocked": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
                                    c_void_p, c_void_p]),
     "rlq_linear_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
-    "rlq_workspace_clear": (c_int, [c_void_p, c_size_t, c_void_p]),
     "rlq_linear_affine": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int, c_int,
                                   c_void_p, c_size_t, c_void_p]),
     "rlq_linear_affine_kernel": (c_int, [c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p,

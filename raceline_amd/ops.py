@@ -114,9 +114,8 @@ def repack_blocked(w_blk: torch.Tensor, s_blk: torch.Tensor, b_blk: torch.Tensor
 
 
 class _Workspaces:
-    """One zero-filled scratch buffer per device, grown on demand. Kernels leave its
-    counter area zeroed, so it is cleared only when (re)allocated. Calls that use it must
-    not overlap on two streams of one device."""
+    """One scratch buffer per device, grown on demand (its contents are not kept between
+    calls). Calls that use it must not overlap on two streams of one device."""
 
     def __init__(self):
         self._bufs = {}
@@ -129,7 +128,7 @@ class _Workspaces:
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
-                buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 

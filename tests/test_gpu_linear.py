@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from tests.qdata import make_layer, make_x, packed_layout_np, to_dev, upload, upload_mlx
+from tests.qdata import make_layer, make_x, packed_layout_np, sample_cols, to_dev, upload, upload_mlx
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -117,8 +117,20 @@ def test_rows_do_not_depend_on_other_rows(gpu):
         np.testing.assert_array_equal(y_one[0], y_all[m])
 
 
+def test_gemm_rows_do_not_depend_on_other_rows(gpu):
+    """The prefill kernel keeps the same rule: rows 50..119 alone (M = 70) give the same
+    bits as inside M = 200, wherever the 128-row tiles fall."""
+    M, K, N = 200, 2048, 640
+    q, s, b = make_layer(15, N, K)
+    x = make_x(16, M, K)
+    wt = upload(q, s, b, "f16", gpu)
+    y_all = _run(gpu, x, wt, kernel=2)
+    y_sub = _run(gpu, x[50:120], wt, kernel=2)
+    np.testing.assert_array_equal(y_sub, y_all[50:120])
+
+
 def test_repeat_calls_reuse_workspace(gpu):
-    """Split-K counters reset themselves: repeated calls give identical results."""
+    """Repeated calls give identical results (no state carried between calls)."""
     M, K, N = 1, 4096, 1024
     q, s, b = make_layer(13, N, K)
     x = make_x(14, M, K)
@@ -206,3 +218,24 @@ def test_group_sums(gpu):
                 acc = np.float32(acc + np.float32(v))
             ref[m, g] = acc
     np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,K,N", O.REFERENCE_TEST_CASES)
+def test_reference_correctness_cases(gpu, M, K, N):
+    """The reference's own correctness cases (tests/test_linear.mm:440-446): layers drawn
+    with its generator (bf16 scales, blocked file layout), checked on sampled columns
+    against the fp64 dequant+matmul, through both weight producers."""
+    import torch
+
+    from raceline_amd import ops
+
+    q, s, b, x = O.reference_test_case(M, K, N)
+    cols = sample_cols(N, 256, seed=M)
+    ref = O.linear_affine_f64(x, q, s, b, "bf16", cols=cols)
+    w_blk, s_blk, b_blk, n_pad, offs = O.pack_blocked([(q, s, b)])
+    pw_blk = ops.pack_blocked(to_dev(w_blk, gpu), to_dev(s_blk.view(np.int16), gpu), to_dev(b_blk.view(np.int16), gpu),
+                              K, n_pad, 0, N, scale_dtype=torch.bfloat16)
+    pw_mlx = upload(q, s, b, "bf16", gpu)
+    for name, pw in (("blocked", pw_blk), ("mlx", pw_mlx)):
+        y = _run(gpu, x, pw)
+        O.check_close(y[:, cols], ref, TOL, f"reference case M={M} K={K} N={N} via {name}")

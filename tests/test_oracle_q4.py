@@ -252,3 +252,30 @@ def test_xorshift_generator_properties():
     assert len(set(vals)) == 1000 and all(0 < v < (1 << 64) for v in vals)
     u = [float(g.uniform(0.001, 0.012)) for _ in range(1000)]
     assert min(u) >= 0.001 and max(u) < 0.012
+
+
+def test_xorshift_stream_equals_serial_steps():
+    """The block-jump stream (T^L by byte tables) against plain serial xorshift64 steps,
+    across several block boundaries; the state continues identically afterwards."""
+    a, b = O.XorShift64(), O.XorShift64()
+    fast = a.stream(3 * a._BLOCK + 123)
+    slow = np.array([b.next() for _ in range(len(fast))], dtype=np.uint64)
+    np.testing.assert_array_equal(fast, slow)
+    assert a.state == b.state and a.next() == b.next()
+    # vectorised uniform == the scalar one on the same outputs
+    c, d = O.XorShift64(7), O.XorShift64(7)
+    r = c.stream(64)
+    assert [float(v) for v in O.XorShift64.uniform_of(r, -2.0, 2.0)] == [float(d.uniform(-2.0, 2.0)) for _ in range(64)]
+
+
+def test_reference_test_case_draws():
+    """Inputs of the reference's correctness cases have the distribution its test states
+    (tests/test_linear.mm:80-88,145): codes 0..15, s in [0.001, 0.012), b = -7.5 s +
+    U(-0.01, 0.01), x = fp16 U(-2, 2); the first codes are the generator's first outputs."""
+    q, s, b, x = O.reference_test_case(3, 256, 512)
+    g = O.XorShift64()
+    assert [int(v) for v in q[0, :16]] == [g.next() & 15 for _ in range(16)]
+    sf, bf = O.bf16_bits_to_f32(s), O.bf16_bits_to_f32(b)
+    assert q.max() <= 15 and sf.min() >= 0.00099 and sf.max() <= 0.012 + 2.0 ** -14   # one bf16 step
+    assert np.all(np.abs(bf + 7.5 * sf) <= 0.0101 + 0.01 * np.abs(bf))
+    assert x.dtype == np.float16 and np.abs(x).max() <= 2.0 and x.shape == (3, 256)

@@ -12,8 +12,8 @@ re-reads. Steps are replayed from HIP graphs (one per copy) so that host launch 
 not pace the GPU. value = algorithmic bytes of the step / measured time per step.
 
 Also reported under "detail": the M=5 layer, the 27B layer at M=1 and M=8 (config 3), the
-27B prefill layer at M=2048 (config 4, TFLOP/s against the dense fp16 MFMA peak), each
-projection's kernel time, and the CPU baseline: the reference's numpy dequant + fp32
+27B prefill layer at M=2048 (config 4, TFLOP/s against the dense fp16 MFMA peak), the MoE
+layer at T=1 and T=512 (config 5), each projection's kernel time, and the CPU baseline: the reference's numpy dequant + fp32
 matmul (oracle.linear_affine_cpu_f32) on a bounded sample, timed on this host.
 """
 
@@ -123,6 +123,82 @@ def time_steps(runner, steps, warmup):
         end.record()
         torch.cuda.synchronize()
     return start.elapsed_time(end) / 1e3 / steps      # seconds per step
+
+
+class StepGraphs:
+    """HIP graphs of an arbitrary step: one graph per weight copy, captured and replayed on
+    one stream that the timing events bracket (same scheme as LayerRunner)."""
+
+    def __init__(self, steps_per_copy):
+        import torch
+
+        self.torch = torch
+        self.stream = torch.cuda.Stream()
+        with torch.cuda.stream(self.stream):
+            for fn in steps_per_copy:
+                fn()
+        torch.cuda.synchronize()
+        self.step_graphs = []
+        for fn in steps_per_copy:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.stream):
+                fn()
+            self.step_graphs.append(g)
+        self.round_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.round_graph, stream=self.stream):
+            for fn in steps_per_copy:
+                fn()
+        torch.cuda.synchronize()
+
+    run_steps = LayerRunner.run_steps
+
+
+MOE_EXPERT_BYTES = 1769472   # codes + fp16 s/b of one expert's gate_up [1024][2048] and down [2048][512]
+
+
+def bench_moe(device, steps, warmup):
+    """the MoE layer (H=2048, E=256 + shared, I=512, top-8, norm_topk) at
+    T=1 and T=512, all experts resident, >= 1 GiB of rotating weight copies. One step =
+    route + gate/up (gather, SwiGLU fused) + down + combine into h. Bytes follow the
+    algorithmic count distinct_experts * 1,769,472 + A*(2H*2 + 2I*4 + I*2 + H*4)."""
+    import torch
+
+    from raceline_amd import ops, synth
+    from raceline_amd.configs import MOE
+
+    E, H, I, topk = MOE["E"], MOE["H"], MOE["I"], MOE["topk"]
+    per_copy = ops.packed_bytes(H, (E + 1) * 2 * I) + ops.packed_bytes(I, (E + 1) * H)
+    copies = max(2, -(-CACHE_DEFEAT_BYTES // per_copy))
+    log(f"[bench] building {copies} copies of the MoE experts ({per_copy / 1e6:.1f} MB each)")
+    mws = []
+    for c in range(copies):
+        gu = synth.random_affine((E + 1) * 2 * I, H, 500 + 2 * c, device, packed=False)
+        dn = synth.random_affine((E + 1) * H, I, 501 + 2 * c, device, packed=False)
+        mws.append(ops.pack_moe(gu, dn, E, H, I))
+        del gu, dn
+    out = {}
+    for T in MOE["tokens"]:
+        x = synth.random_activations(T, H, 600 + T, device)
+        g = torch.Generator(device=device)
+        g.manual_seed(601 + T)
+        logits = torch.randn((T, E + 1), generator=g, device=device, dtype=torch.float32)
+        h = torch.zeros((T, H), dtype=torch.float32, device=device)
+        ws = torch.empty(ops.moe_workspace_bytes(T, E, topk, H, I), dtype=torch.uint8, device=device)
+        fns = [(lambda mw=mw: ops.moe(x, logits, mw, topk, h, workspace=ws)) for mw in mws]
+        sg = StepGraphs(fns)
+        t = time_steps(sg, steps, warmup)
+        distinct = int(torch.unique(ops.moe_route(logits, E, topk).sel).numel())
+        A = T * (topk + 1)
+        nbytes = distinct * MOE_EXPERT_BYTES + A * (2 * H * 2 + 2 * I * 4 + I * 2 + H * 4)
+        flops = 2 * A * 3 * H * I
+        out[f"moe_t{T}"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
+                            "TFLOP/s": round(flops / t / 1e12, 2), "distinct_experts": distinct,
+                            "algorithmic_bytes": nbytes}
+        log(f"[bench] MoE T={T}: {t * 1e6:.1f} us/step, {nbytes / t / 1e9:.0f} GB/s ({distinct} experts)")
+        del sg
+    del mws
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_kernel(layers, shapes, M, idx, device, launches, kernel=0, outliers=0.0):
@@ -337,6 +413,7 @@ def main():
         log(f"[bench] 27B prefill: {flops / tp / 1e12:.1f} TFLOP/s")
         del rp, l27
         torch.cuda.empty_cache()
+        detail.update(bench_moe(dev, args.steps, args.warmup))
 
     cpu = None
     if not args.quick and not args.no_cpu:

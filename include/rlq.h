@@ -107,6 +107,67 @@ int rlq_group_sums(const void *x, int x_stride, int M, int K, float *gsum, void 
  * entry point: the matmuls never materialise W. */
 int rlq_dequant_affine(const void *packed, int scale_dtype, int K, int N, float *out, void *stream);
 
+/* ---------------------------------------------------------------- mixture of experts */
+
+/* A MoE MLP of E routed experts plus one shared expert (number E), each a gate/up matrix
+ * [2I][H] (I gate rows, then I up rows) and a down matrix [H][I], stacked over the E + 1
+ * experts as the reference stacks them (tools/quantize.py:168-228, shared expert last):
+ * gate_up [(E+1)*2I][H], down [(E+1)*H][I], 4-bit affine with groups of 64. A token goes
+ * to its topk best experts and the shared one: S = topk + 1 assignments, a = t*S + slot.
+ * Replaces Engine::encode_moe (src/engine.mm:965-1059) with kernels/moe.metal and
+ * linear_q4n_moe (kernels/linear.metal:254-308) for the affine format. Sizes: E <= 1023,
+ * topk <= 16, H and I multiples of 64 up to 24576. */
+
+/* The gate/up stack (MLX layout, codes [(E+1)*2I][H/8], s and b [(E+1)*2I][H/64]) ->
+ * packed, with each expert's gate and up rows interleaved 8 and 8 per 16-row tile (so one
+ * tile yields both halves of SwiGLU). Bytes: rlq_packed_affine_bytes(H, (E+1)*2I). The
+ * down stack is packed with rlq_pack_affine(w, s, b, I, (E+1)*H, ...). */
+int rlq_pack_moe_gate_up(const uint32_t *w, const void *s, const void *b, int H, int E1, int I, void *packed,
+                         void *stream);
+
+/* Upper bound on the work items of a call (size of `items`, in units of 4 ints). */
+size_t rlq_moe_max_items(int T, int E, int topk);
+
+/* Routing (kernels/moe.metal:40-140). logits fp32 [T][logit_stride], columns 0..E-1 the
+ * router's, column E the shared expert's gate. Writes, for a = t*S + slot:
+ *   sel[a], w[a]  the expert and weight of each assignment: slots 0..topk-1 the chosen
+ *                 experts in falling order of logit (equal logits: lower expert first),
+ *                 weights softmax over all E logits, renormalised over the chosen ones
+ *                 when norm_topk; slot topk the shared expert, weight sigmoid(logit[E]);
+ *   tok[r], inv[a] the counting sort by expert: sorted row r holds token tok[r], and
+ *                 assignment a is sorted row inv[a]; within an expert, rows in token order;
+ *   items         (expert, first row, rows <= 16, 0) per work item, experts ascending;
+ *   *n_items      their number (device memory).
+ * sel, w, tok, inv: T*S entries; items: rlq_moe_max_items(T, E, topk) * 4 ints, 16-byte aligned. */
+int rlq_moe_route(const float *logits, int logit_stride, int T, int E, int topk, int norm_topk, int *sel, float *w,
+                  int *tok, int *inv, int *items, int *n_items, void *stream);
+
+/* act[r][i] = half(silu(g) * u) for every sorted row r, where (g, u) = x[tok[r]] times the
+ * gate and up rows i of the row's expert (kernels/ops.metal:446-455 with unit column
+ * scales, as for affine matrices, src/engine.mm:937-940). x fp16 [T][x_stride]; act fp16
+ * [T*S][act_stride]. The gather of kernels/moe.metal:143-155 is fused (rows are read
+ * through tok). */
+int rlq_moe_gate_up(const void *x, int x_stride, int T, int H, int I, int E, int topk, const void *packed_gu,
+                    int scale_dtype, const int *tok, const int *items, const int *n_items, void *act, int act_stride,
+                    void *stream);
+
+/* y[r][d] = act[r] times down row d of the row's expert, fp32 [T*S][y_stride]. */
+int rlq_moe_down(const void *act, int act_stride, int T, int H, int I, int E, int topk, const void *packed_dn,
+                 int scale_dtype, const int *items, const int *n_items, float *y, int y_stride, void *stream);
+
+/* h[t][d] += sum over slots s (in order) of w[t*S+s] * y[inv[t*S+s]][d]
+ * (kernels/moe.metal:157-174). */
+int rlq_moe_combine(const float *y, int y_stride, const int *inv, const float *w, int T, int topk, int H, float *h,
+                    int h_stride, void *stream);
+
+/* The whole MoE MLP: route, gate/up + SwiGLU, down, combine into h (fp32 [T][h_stride],
+ * accumulated like the reference's residual stream). The workspace holds the routing,
+ * act and y; rlq_moe_workspace_bytes sizes it (256-byte aligned, no initialisation). */
+size_t rlq_moe_workspace_bytes(int T, int E, int topk, int H, int I);
+int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, int T, int E, int topk, int norm_topk,
+            int H, int I, const void *packed_gu, const void *packed_dn, int scale_dtype, float *h, int h_stride,
+            void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

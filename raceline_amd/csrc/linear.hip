@@ -9,47 +9,23 @@
 // matrix cores as exact fp16 values and the scale and bias are applied per group
 // to the fp32 partial product.
 //
-// Matrix cores: v_mfma_f32_16x16x32_f16 (wave64), A = activations (rows = tokens), B =
-// codes (cols = output features):
-//   A (16 x 32): lane l holds row l%16, k = 8*(l/16) .. +7
-//   B (32 x 16): lane l holds col l%16, k = 8*(l/16) .. +7
-//   D (16 x 16): lane l holds col l%16, rows 4*(l/16) .. +3
-// One group of 64 inputs is two MFMA steps s = 0, 1 (k = 64g + 32s .. +31); lane (c, j) =
-// (l%16, l/16) feeds uint32 word 8g + 4s + j of row c (k = 64g + 32s + 8j .. +7).
-//
-// Packed device layout (made once at upload, from the MLX layout or the .rlm blocked
-// layout; see include/rlq.h), for tiles t of 16 output rows, G = K/64 groups padded to
-// G4 = ceil(G/4) quads, and group pairs p (groups 2p, 2p+1):
-//   codes: 1024 bytes per (t, p) at ((t*2*G4 + p) * 64 + l) * 16: lane l = 16j + c holds
-//          words (8g + 4s + j of row 16t + c) for (g, s) = (2p,0), (2p,1), (2p+1,0), (2p+1,1)
-//          (tools/convert.py:82-89 nibble order);
-//   scale/bias: after the codes, 16 bytes per (t, quad q, row c) at ((t*G4 + q)*16 + c)*16:
-//          s | b << 16 for groups 4q .. 4q+3;
-// rows beyond N and groups beyond G zero. One 16-byte load per lane brings a lane its
-// operands for two groups, and a wave's loads for consecutive group pairs are
-// consecutive kilobytes: a plain stream for the memory system.
-#include "rlq_common.h"
+// The packed layout, the MFMA operand layout and the operand trick are described in
+// q4_tile.h.
+#include "q4_tile.h"
 #include "../../include/rlq.h"
 
 #include <algorithm>
 
 namespace rlq {
 
-constexpr int kGroup = 64;
-
 constexpr int kMaxTiles = 32768;                                   // N <= 16 * kMaxTiles
-
-__host__ __device__ inline int tiles_of(int N) { return (N + 15) / 16; }
-__host__ __device__ inline int quads_of(int K) { return (K / kGroup + 3) / 4; }
-static inline size_t packed_code_bytes(int K, int N) { return (size_t)tiles_of(N) * quads_of(K) * 2048; }
-static inline size_t packed_bytes(int K, int N) { return (size_t)tiles_of(N) * quads_of(K) * 2304; }
 
 // ================================================================== packing (upload)
 
 // MLX layout (codes uint32 [N][K/8], scales and biases [N][G]) -> packed. One thread per
 // 16-byte piece of codes (tile t, pair p, lane l); threads of lane < 16 of even pairs
 // also write the scale/bias quad of their row.
-__global__ void pack_mlx_kernel(const uint32_t *w, const uint16_t *s, const uint16_t *b, int K, int N,
+__global__ void pack_mlx_kernel(const uint32_t *w, const uint16_t *s, const uint16_t *b, int K, int N, int il,
                                 u32x4 *codes, u32x4 *sb) {
   const int G = K / kGroup, G4 = quads_of(K), GP = 2 * G4;
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;   // ((t * GP + p) * 64 + l)
@@ -58,9 +34,10 @@ __global__ void pack_mlx_kernel(const uint32_t *w, const uint16_t *s, const uint
   const size_t tp = i >> 6;
   const int t = (int)(tp / GP), p = (int)(tp - (size_t)t * GP);
   const int c = l & 15, j = l >> 4, n = 16 * t + c;
+  const int src = il ? gate_up_source_row(n, il) : n;   // il: the gate/up interleave of a MoE stack
   u32x4 v = {};
   if (n < N) {
-    const uint32_t *row = w + (size_t)n * (K / 8);
+    const uint32_t *row = w + (size_t)src * (K / 8);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int g = 2 * p + (e >> 1), sx = e & 1;
@@ -75,7 +52,7 @@ __global__ void pack_mlx_kernel(const uint32_t *w, const uint16_t *s, const uint
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int g = 4 * q + e;
-        e4[e] = g < G ? ((uint32_t)s[(size_t)n * G + g] | ((uint32_t)b[(size_t)n * G + g] << 16)) : 0u;
+        e4[e] = g < G ? ((uint32_t)s[(size_t)src * G + g] | ((uint32_t)b[(size_t)src * G + g] << 16)) : 0u;
       }
     }
     sb[((size_t)t * G4 + q) * 16 + c] = e4;
@@ -204,22 +181,8 @@ __global__ void dequant_kernel(const u32x4 *codes, const u32x4 *sb, int K, int N
 // come from an MFMA against a constant operand, which lands them in the accumulator
 // layout, and every weight load of a wave is issued before its first multiply.
 //
-// Operand trick: a uint32 of eight codes becomes four fp16 pairs with five ops,
-//   d0 = u & 0x000F000F -> (q0, q4)          d1 = u & 0x00F000F0 -> (16 q1, 16 q5)
-//   d2 = (u>>8) & 0x000F000F -> (q2, q6)     d3 = (u>>8) & 0x00F000F0 -> (16 q3, 16 q7)
-// each half being the subnormal (code or 16 * code) * 2^-24, exact. The activation
-// operand carries the same element order with the odd elements divided by 16:
-//   (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16),
-// so one MFMA step sums x_e * q_e * 2^-24 over the eight elements. (x/16 is exact unless
-// |x| < 2^-10, where it rounds to the fp16 subnormal grid: an error below 2^-25 * 16 * 15
-// per such element, far under the 1e-3 bar.) The accumulator carries the same 2^-24:
-// acc += s * part + b * (gsum * 2^-24), both exact rescalings, and is multiplied by 2^24
-// once at the end.
+// The operand trick and the MFMA group sums are described in q4_tile.h.
 constexpr int kGemvMaxM = 8;
-constexpr int kBufFlags = 0x00020000;             // buffer descriptor word 3 for raw 32-bit accesses
-constexpr int kNonTemporal = 2;                   // buffer load cache policy: stream, do not keep
-constexpr float kTwoM24 = 5.9604644775390625e-8f; // 2^-24
-
 struct GemvArgs {
   const _Float16 *x;
   const u32x4 *codes;
@@ -227,44 +190,6 @@ struct GemvArgs {
   float *y;
   int x_stride, M, K, N, y_stride;
 };
-
-__device__ __forceinline__ half8 nib8_to_half8_oddx16(uint32_t u) {
-  const uint32_t t = u >> 8;
-  u32x4 d;
-  d[0] = u & 0x000F000Fu;
-  d[1] = u & 0x00F000F0u;
-  d[2] = t & 0x000F000Fu;
-  d[3] = t & 0x00F000F0u;
-  return __builtin_bit_cast(half8, d);
-}
-
-// eight consecutive activations -> operand order (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16)
-__device__ __forceinline__ u32x4 prep_x8(u32x4 p) {
-  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-  const half2v sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
-  u32x4 r;
-  r[0] = __builtin_amdgcn_perm(p[2], p[0], 0x05040100u);  // (x0, x4)
-  r[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(p[2], p[0], 0x07060302u)) * sixteenth);
-  r[2] = __builtin_amdgcn_perm(p[3], p[1], 0x05040100u);  // (x2, x6)
-  r[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(p[3], p[1], 0x07060302u)) * sixteenth);
-  return r;
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kBufFlags);
-}
-
-// acc += float(s16) * p with the 16-bit float taken from the low or high half of a packed pair
-template <int SD, int HI>
-__device__ __forceinline__ float fma_scale(uint32_t pr, float p, float acc) {
-  if constexpr (SD == 0) {
-    const _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)(HI ? (pr >> 16) : (pr & 0xFFFFu)));
-    return __builtin_fmaf(static_cast<float>(v), p, acc);
-  } else {
-    const float v = __uint_as_float(HI ? (pr & 0xFFFF0000u) : (pr << 16));
-    return __builtin_fmaf(v, p, acc);
-  }
-}
 
 // Groups per wave: 16, or 24 when 16 would need more than 16 waves.
 static int gemv_gpw(int K) { return 4 * quads_of(K) <= 16 * 16 ? 16 : 24; }
@@ -289,46 +214,16 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
   const int t = blockIdx.x;
   const int n = 16 * t + c16;
   const int M = a.M;
-  float *red = reinterpret_cast<float *>(lds);                              // [waves-1][64][4]
+  f32x4 *red = reinterpret_cast<f32x4 *>(lds);                              // [waves-1][64]
 
-  // this wave's groups [wg0, wg0 + GPW) of the padded range; descriptors cover exactly
-  // its part of the packed matrix, so loads past the end return zeros
+  // this wave's groups [wg0, wg0 + GPW) of tile t; wn of them are real
   const int wg0 = wave * GPW;
-  const int wq1 = min(4 * G4, wg0 + GPW);
-  const int wn = max(0, min(G, wg0 + GPW) - wg0);       // real groups of this wave
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.codes + ((size_t)t * 2 * G4 + wg0 / 2) * 64, (uint32_t)(wq1 - wg0) / 2u * 1024u);
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sb + ((size_t)t * G4 + wg0 / 4) * 16, (uint32_t)(wq1 - wg0) / 4u * 256u);
+  const int wn = max(0, min(G, wg0 + GPW) - wg0);
+  const WaveTile wt = wave_tile(a.codes, a.sb, t, G4, wg0, GPW);
   const uint32_t xrange = wn > 0 ? (uint32_t)((M - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
 
-  u32x4 wq[GPW / 2], sq[GPW / 4];
-  auto issue_w = [&]() {
-#pragma unroll
-    for (int pp = 0; pp < GPW / 2; ++pp)
-      wq[pp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, 16u * lane, (uint32_t)pp * 1024u, kNonTemporal));
-#pragma unroll
-    for (int qq = 0; qq < GPW / 4; ++qq)
-      sq[qq] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16u * c16, (uint32_t)qq * 256u, kNonTemporal));
-  };
-
-  // The group sums come from an MFMA against the constant (2^-24, 2^-24, 16 * 2^-24,
-  // 16 * 2^-24, ...), which undoes the 1/16 of the odd elements. An MFMA output row depends
-  // only on its own operand row, so a token's result is the same for every M.
-  const half8 ones = __builtin_bit_cast(half8, u32x4{0x00010001u, 0x00100010u, 0x00010001u, 0x00100010u});
   f32x4 acc = {};
-  auto step = [&](int jg, const half8 *af) {
-    f32x4 p = {}, gsv = {};
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], nib8_to_half8_oddx16(wq[jg >> 1][2 * (jg & 1) + s]), p, 0, 0, 0);
-      gsv = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, gsv, 0, 0, 0);
-    }
-    const uint32_t pr = sq[jg >> 2][jg & 3];
-    // MAXM = 1: only token row 0 is live (lanes 0..15, element 0)
-#pragma unroll
-    for (int r = 0; r < (MAXM == 1 ? 1 : 4); ++r) acc[r] = fma_scale<SD, 1>(pr, gsv[r], fma_scale<SD, 0>(pr, p[r], acc[r]));
-  };
-
   if constexpr (MAXM == 1) {
     // One token: the wave's activation row is loaded first (the loads complete in issue
     // order, so waiting for it does not wait for the weights), then every weight load is
@@ -338,14 +233,14 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
     constexpr int XCH = GPW * 8;                 // chunks of 8 activations in the wave's range
     constexpr int XPER = (XCH + 63) / 64;
     _Float16 *xs = reinterpret_cast<_Float16 *>(lds + (size_t)(waves - 1) * 64 * 16) + (size_t)wave * GPW * kGroup;
-    u32x4 xr[XPER];
+    u32x4 xr[XPER], wq[GPW / 2], sq[GPW / 4];
 #pragma unroll
     for (int i = 0; i < XPER; ++i) {
       const int chunk = lane + 64 * i;
       const bool in_range = chunk < XCH && (chunk >> 3) < wn;
-      xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, in_range ? 16u * chunk : 0x7FFFFFF0u, 0, 0));
+      xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, in_range ? 16u * chunk : kFarOffset, 0, 0));
     }
-    issue_w();
+    issue_tile_loads<GPW>(wt, lane, wq, sq);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < XPER; ++i) {
@@ -367,55 +262,24 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) an[s] = *reinterpret_cast<const half8 *>(xa + (jg + 1) * kGroup + 32 * s);
       }
-      step(jg, af);
+      group_step<GPW, SD, 1>(acc, af, wq, sq, jg);
       __builtin_amdgcn_sched_barrier(0);   // one group at a time: bounded register use
     }
   } else {
-    // Several tokens: activation operands come straight from memory (L2-resident, shared
-    // by every workgroup), two groups ahead, and are put in operand order in registers;
-    // lanes whose token row is >= M read zeros (out of the descriptor's range).
-    const bool live = c16 < M;
-    const uint32_t xoff = (uint32_t)c16 * a.x_stride * 2u + 16u * j4;
-    auto ldx = [&](int jg, int s) -> u32x4 {
-      const bool ok = live && jg < wn;
-      return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                           rx, ok ? xoff + (uint32_t)(jg * kGroup + 32 * s) * 2u : 0x7FFFFFF0u, 0, 0));
-    };
-    u32x4 ax[3][2];
-#pragma unroll
-    for (int d = 0; d < 2; ++d)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) ax[d][s] = ldx(d, s);
-    issue_w();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int jg = 0; jg < GPW; ++jg) {
-      if (jg + 2 < GPW) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) ax[(jg + 2) % 3][s] = ldx(jg + 2, s);
-      }
-      const half8 af[2] = {__builtin_bit_cast(half8, prep_x8(ax[jg % 3][0])),
-                           __builtin_bit_cast(half8, prep_x8(ax[jg % 3][1]))};
-      step(jg, af);
-    }
+    // Several tokens: lane (c16, j4) reads token row c16's activations from memory;
+    // rows >= M read zeros.
+    acc = tile_dot_rows<GPW, SD>(wt, rx, (uint32_t)c16 * a.x_stride * 2u + 16u * j4, c16 < M, wn, lane);
   }
 
-  // waves 1.. hand their partials to wave 0, which adds them in wave order; lane (c16, j4)
-  // holds token rows 4 j4 .. 4 j4 + 3 of output n
-  if (wave > 0) *reinterpret_cast<f32x4 *>(red + ((wave - 1) * 64 + lane) * 4) = acc;
-  __syncthreads();
+  // lane (c16, j4) holds token rows 4 j4 .. 4 j4 + 3 of output n
+  acc = reduce_waves(acc, red, wave, waves, lane);
   if (wave == 0 && n < a.N && 4 * j4 < M) {
-    for (int w = 1; w < waves; ++w) {
-      const f32x4 o = *reinterpret_cast<const f32x4 *>(red + ((w - 1) * 64 + lane) * 4);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) acc[v] += o[v];
-    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = 4 * j4 + v;
       if (m < M) {
         float *dst = a.y + (size_t)m * a.y_stride + n;
-        const float val = acc[v] * kTwo24;
+        const float val = acc[v];
         *dst = ACC ? *dst + val : val;
       }
     }
@@ -576,7 +440,7 @@ __global__ __launch_bounds__(256) void gemm_q4a_kernel(GemmArgs a) {
 #pragma unroll
           for (int s = 0; s < 2; ++s) pp = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bf[ft][s], pp, 0, 0, 0);
           const uint32_t pr = sq[ft][2 * (p & 1) + gg];
-          const float sc = scale_f32<SD>((uint16_t)(pr & 0xFFFFu)) * kTwo24;
+          const float sc = scale_f32<SD>((uint16_t)(pr & 0xFFFFu));
           const float bi = scale_f32<SD>((uint16_t)(pr >> 16));
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[mt][ft][r] += sc * pp[r] + bi * gq[r];
@@ -662,18 +526,31 @@ size_t rlq_packed_affine_bytes(int K, int N) {
   return packed_bytes(K, N);
 }
 
-int rlq_pack_affine(const uint32_t *w, const void *s, const void *b, int K, int N, void *packed, void *stream) {
-  RLQ_REQUIRE(N >= 1 && K >= kGroup && K % kGroup == 0, "rlq_pack_affine: bad sizes K=%d N=%d", K, N);
-  RLQ_REQUIRE(w && s && b && packed, "rlq_pack_affine: null pointer argument");
-  RLQ_REQUIRE(aligned(w, 4) && aligned(packed, 16), "rlq_pack_affine: misaligned w or packed");
-  RLQ_REQUIRE(aligned(s, 2) && aligned(b, 2), "rlq_pack_affine: misaligned scales or biases");
+static int pack_mlx(const char *who, const uint32_t *w, const void *s, const void *b, int K, int N, int il,
+                    void *packed, void *stream) {
+  RLQ_REQUIRE(N >= 1 && K >= kGroup && K % kGroup == 0, "%s: bad sizes K=%d N=%d", who, K, N);
+  RLQ_REQUIRE(w && s && b && packed, "%s: null pointer argument", who);
+  RLQ_REQUIRE(aligned(w, 4) && aligned(packed, 16), "%s: misaligned w or packed", who);
+  RLQ_REQUIRE(aligned(s, 2) && aligned(b, 2), "%s: misaligned scales or biases", who);
   const size_t pieces = (size_t)tiles_of(N) * 2 * quads_of(K) * 64;
   auto codes = static_cast<u32x4 *>(packed);
   auto sb = reinterpret_cast<u32x4 *>(static_cast<char *>(packed) + packed_code_bytes(K, N));
   pack_mlx_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
-      w, static_cast<const uint16_t *>(s), static_cast<const uint16_t *>(b), K, N, codes, sb);
+      w, static_cast<const uint16_t *>(s), static_cast<const uint16_t *>(b), K, N, il, codes, sb);
   RLQ_HIP(hipGetLastError());
   return 0;
+}
+
+int rlq_pack_affine(const uint32_t *w, const void *s, const void *b, int K, int N, void *packed, void *stream) {
+  return pack_mlx("rlq_pack_affine", w, s, b, K, N, 0, packed, stream);
+}
+
+int rlq_pack_moe_gate_up(const uint32_t *w, const void *s, const void *b, int H, int E1, int I, void *packed,
+                         void *stream) {
+  RLQ_REQUIRE(E1 >= 1 && I >= 8 && I % 8 == 0, "rlq_pack_moe_gate_up: %d experts of I=%d (I must be a multiple of 8)",
+              E1, I);
+  RLQ_REQUIRE((long long)E1 * 2 * I <= 16LL * kMaxTiles, "rlq_pack_moe_gate_up: %d x %d rows is too many", E1, 2 * I);
+  return pack_mlx("rlq_pack_moe_gate_up", w, s, b, H, E1 * 2 * I, I, packed, stream);
 }
 
 int rlq_pack_affine_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const uint16_t *b_blk, int K, int n_pad,

@@ -1,0 +1,476 @@
+// Mixture-of-experts MLP on gfx950: routing, the grouped expert matmuls over 4-bit affine
+// expert stacks, SwiGLU and the combine, following kernels/moe.metal and
+// src/engine.mm:965-1059 of the reference.
+//
+// A token goes to `topk` of E routed experts (falling logit, equal logits: the lower
+// expert first) plus the shared expert, number E; S = topk + 1 assignments per token,
+// assignment a = t * S + slot. The routing sorts the assignments by expert into "rows";
+// each expert's rows are consecutive, and an expert's rows are cut into work items of at
+// most 16 rows (the MFMA tile height). The grouped kernels run one workgroup per (item,
+// 16-row weight tile) over the expert's matrices in the stacked tensors; the combine adds
+// each token's S results to its residual row in slot order.
+//
+// Differences from the reference, all of them MI355X choices:
+//  - rows within an expert are placed in token order (the reference places them with
+//    atomics in no particular order, moe.metal:133-139); nothing depends on it, but the
+//    order is now reproducible run to run;
+//  - the gather of the routed rows is fused into the gate/up kernel (it reads x through
+//    the row -> token map), and SwiGLU into its epilogue (the gate/up stack is packed so
+//    one 16-row tile holds 8 gate rows and the matching 8 up rows);
+//  - there is no indirect dispatch: grids are sized for the most items a call can have,
+//    and workgroups past the item count the routing wrote exit at once.
+// A row's result depends only on its own token (MFMA rows are independent), so the
+// layer's output for a token does not depend on the other tokens of the call.
+#include "q4_tile.h"
+#include "../../include/rlq.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace rlq {
+
+constexpr int kItemRows = 16;     // rows per work item: the MFMA tile height
+constexpr int kMaxTopk = 16;
+constexpr int kMaxExperts = 1023; // E; E + 1 <= 1024 (one thread per expert in the sort)
+
+// Most work items a call can have: sum over experts of ceil(rows_e / 16) <= A / 16 + the
+// number of experts with rows, which is at most min(E + 1, A).
+static inline int moe_max_items(int T, int E, int topk) {
+  const long long A = (long long)T * (topk + 1);
+  return (int)(A / kItemRows + std::min<long long>(E + 1, A));
+}
+
+// ------------------------------------------------------------------ routing: top-k
+
+// One wave per token. Lane l holds logits l, l + 64, ...; repeated wave-wide argmax with
+// ties to the lower expert (kernels/moe.metal:75-91). Weights: exp(l - max) over the
+// softmax denominator of all E logits, or over the chosen ones when norm_topk
+// (moe.metal:92-102); the shared slot gets sigmoid(logit[E]) (moe.metal:103-104).
+template <int EPL>
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int stride, int T, int E, int topk,
+                                                       int norm_topk, int *sel, float *w) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int S = topk + 1;
+  const float *row = logits + (size_t)t * stride;
+  float v[EPL];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    const float l = e < E ? row[e] : -INFINITY;
+    v[j] = l == l ? l : -INFINITY;            // a NaN logit ranks last
+    m = fmaxf(m, v[j]);
+  }
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  float z = 0.0f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) z += (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
+  for (int o = 32; o >= 1; o >>= 1) z += __shfl_xor(z, o);
+
+  // Chosen experts are tracked in `taken`, so every pick is a distinct expert < E even
+  // when logits tie at -inf (topk <= E guarantees a candidate).
+  float top[kMaxTopk];
+  int which[kMaxTopk];
+  uint32_t taken = 0;
+  for (int r = 0; r < topk; ++r) {
+    float bv = -INFINITY;
+    int be = 1 << 30;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && !((taken >> j) & 1u) && (v[j] > bv || (v[j] == bv && e < be))) {
+        bv = v[j];
+        be = e;
+      }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oe = __shfl_xor(be, o);
+      if (ov > bv || (ov == bv && oe < be)) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    top[r] = bv;
+    which[r] = be;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+      if (lane + 64 * j == be) taken |= 1u << j;
+  }
+  if (lane == 0) {
+    float ex[kMaxTopk], sum = 0.0f;
+    for (int r = 0; r < topk; ++r) {
+      ex[r] = expf(top[r] - m);
+      sum += ex[r];
+    }
+    const float denom = norm_topk ? sum : z;
+    for (int r = 0; r < topk; ++r) {
+      sel[t * S + r] = which[r];
+      w[t * S + r] = ex[r] / denom;
+    }
+    sel[t * S + topk] = E;
+    w[t * S + topk] = 1.0f / (1.0f + expf(-row[E]));
+  }
+}
+
+// ------------------------------------------------------------------ routing: sort
+
+// Exclusive prefix sum over the workgroup (1024 threads) of one int per thread.
+__device__ int block_exclusive_scan(int v, int *wave_tot, int *total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(inc, o);
+    if (lane >= o) inc += u;
+  }
+  if (lane == 63) wave_tot[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) {
+      const int c = wave_tot[i];
+      wave_tot[i] = run;
+      run += c;
+    }
+    *total = run;
+  }
+  __syncthreads();
+  const int ex = wave_tot[wave] + inc - v;
+  __syncthreads();   // wave_tot may be reused by the caller's next scan
+  return ex;
+}
+
+// One workgroup of 1024 threads sorts all T*S assignments by expert (a counting sort,
+// moe.metal:109-139) and writes the work list. Within an expert, rows follow token order:
+// token t's row for expert e is off[e] + (tokens before t that chose e), counted with one
+// bitmap per expert over a chunk of tokens and prefix popcounts (a token chooses an expert
+// at most once). LDS: counts and offsets, then per chunk bm[E+1][wpe] and pre[E+1][wpe].
+__global__ __launch_bounds__(1024) void moe_sort_kernel(const int *sel, int T, int E, int S, int wpe, int *tok,
+                                                        int *inv, int4 *items, int *n_items) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  int *cnt = reinterpret_cast<int *>(lds);      // [1024]
+  int *off = cnt + 1024;                        // [1024]
+  int *run = off + 1024;                        // [1024]
+  int *scratch = run + 1024;                    // [32]
+  uint32_t *bm = reinterpret_cast<uint32_t *>(scratch + 32);   // [(E+1) * wpe]
+  uint32_t *pre = bm + (size_t)(E + 1) * wpe;                   // [(E+1) * wpe]
+  const int tid = threadIdx.x;
+  const int A = T * S;
+  const int E1 = E + 1;
+
+  cnt[tid] = 0;
+  run[tid] = 0;
+  __syncthreads();
+  // sel comes from moe_topk_kernel (0 <= sel < E + 1); the clamps keep every index in
+  // range whatever it holds
+  for (int a = tid; a < A; a += 1024) atomicAdd(&cnt[min(max(sel[a], 0), E)], 1);
+  __syncthreads();
+  const int c = tid < E1 ? cnt[tid] : 0;
+  const int o = block_exclusive_scan(c, scratch, scratch + 16);
+  const int ni = (c + kItemRows - 1) / kItemRows;
+  const int io = block_exclusive_scan(ni, scratch, scratch + 17);
+  if (tid < E1) {
+    off[tid] = o;
+    for (int i = 0; i < ni; ++i)
+      items[io + i] = int4{tid, o + i * kItemRows, min(kItemRows, c - i * kItemRows), 0};
+  }
+  if (tid == 0) *n_items = scratch[17];
+  __syncthreads();
+
+  const int chunk = 32 * wpe;                   // tokens per chunk
+  for (int t0 = 0; t0 < T; t0 += chunk) {
+    const int tn = min(chunk, T - t0);
+    for (int i = tid; i < E1 * wpe; i += 1024) bm[i] = 0u;
+    __syncthreads();
+    for (int a = t0 * S + tid; a < (t0 + tn) * S; a += 1024) {
+      const int tl = a / S - t0;
+      atomicOr(&bm[(size_t)min(max(sel[a], 0), E) * wpe + (tl >> 5)], 1u << (tl & 31));
+    }
+    __syncthreads();
+    if (tid < E1) {
+      uint32_t acc = 0;
+      for (int i = 0; i < wpe; ++i) {
+        pre[(size_t)tid * wpe + i] = acc;
+        acc += __popc(bm[(size_t)tid * wpe + i]);
+      }
+    }
+    __syncthreads();
+    for (int a = t0 * S + tid; a < (t0 + tn) * S; a += 1024) {
+      const int t = a / S, tl = t - t0, e = min(max(sel[a], 0), E);
+      const size_t wi = (size_t)e * wpe + (tl >> 5);
+      const int rank = run[e] + (int)pre[wi] + __popc(bm[wi] & ((1u << (tl & 31)) - 1u));
+      const int pos = off[e] + rank;
+      inv[a] = pos;
+      tok[pos] = t;
+    }
+    __syncthreads();
+    if (tid < E1) run[tid] += (int)(pre[(size_t)tid * wpe + wpe - 1] + __popc(bm[(size_t)tid * wpe + wpe - 1]));
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------ grouped expert matmuls
+
+struct MoeArgs {
+  const _Float16 *x;        // gate_up: the token rows [T][x_stride]; down: act [A][x_stride]
+  const int *tok;           // gate_up: row -> token (the fused gather); down: unused
+  const u32x4 *codes;
+  const u32x4 *sb;
+  const int4 *items;
+  const int *n_items;
+  void *out;                // gate_up: act fp16 [A][out_stride]; down: y fp32 [A][out_stride]
+  int x_rows, x_stride, K, tiles_per_expert, out_stride;
+};
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// KIND 0: gate/up with the gather and SwiGLU fused (interleaved stack); KIND 1: down.
+// grid (tiles_per_expert, max_items); block 64 * ceil(4 G4 / GPW).
+template <int GPW, int SD, int KIND>
+__global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int item = blockIdx.y;
+  if (item >= *a.n_items) return;               // uniform: the whole workgroup leaves
+  const int4 it = a.items[item];
+  const int e = it.x, r0 = it.y, rows = it.z;
+  const int waves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, j4 = lane >> 4;
+  const int G = a.K / kGroup, G4 = quads_of(a.K);
+  const int tile = blockIdx.x;
+  const int t = e * a.tiles_per_expert + tile;
+  const int wg0 = wave * GPW;
+  const int wn = max(0, min(G, wg0 + GPW) - wg0);
+  const WaveTile wt = wave_tile(a.codes, a.sb, t, G4, wg0, GPW);
+
+  const bool live = c16 < rows;
+  int xrow = r0 + (live ? c16 : 0);
+  if constexpr (KIND == 0) xrow = a.tok[xrow];
+  const uint32_t xrange = wn > 0 ? (uint32_t)((a.x_rows - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
+  f32x4 acc = tile_dot_rows<GPW, SD>(wt, rx, (uint32_t)xrow * a.x_stride * 2u + 16u * j4, live, wn, lane);
+  acc = reduce_waves(acc, reinterpret_cast<f32x4 *>(lds), wave, waves, lane);
+  if (wave != 0) return;
+  if constexpr (KIND == 0) {
+    // lanes c16 < 8 hold gate features 8 tile + c16, lanes c16 + 8 the matching up ones
+    _Float16 *act = static_cast<_Float16 *>(a.out);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float u = __shfl_xor(acc[v], 8);
+      const int r = 4 * j4 + v;
+      if (c16 < 8 && r < rows)
+        act[(size_t)(r0 + r) * a.out_stride + 8 * tile + c16] = static_cast<_Float16>(silu(acc[v]) * u);
+    }
+  } else {
+    float *y = static_cast<float *>(a.out);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = 4 * j4 + v;
+      if (r < rows) y[(size_t)(r0 + r) * a.out_stride + 16 * tile + c16] = acc[v];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ combine
+
+// h[t][d] += sum over slots s of w[t*S + s] * y[inv[t*S + s]][d], the slots in order
+// (moe.metal:157-174).
+__global__ void moe_combine_kernel(const float *y, int y_stride, const int *inv, const float *w, int T, int S, int H,
+                                   float *h, int h_stride) {
+  const int d = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  if (d >= H || t >= T) return;
+  float acc = 0.0f;
+  for (int s = 0; s < S; ++s) {
+    const int a = t * S + s;
+    acc += w[a] * y[(size_t)inv[a] * y_stride + d];
+  }
+  h[(size_t)t * h_stride + d] += acc;
+}
+
+// ------------------------------------------------------------------ host side
+
+static int expert_gpw(int K) { return 4 * quads_of(K) <= 16 * 16 ? 16 : 24; }
+static int expert_waves(int K) { const int g = expert_gpw(K); return (4 * quads_of(K) + g - 1) / g; }
+
+template <int GPW, int SD, int KIND>
+static int launch_expert_inst(dim3 grid, int threads, hipStream_t st, const MoeArgs &a) {
+  const size_t lds = (size_t)(threads / 64 - 1) * 64 * 16;
+  moe_expert_kernel<GPW, SD, KIND><<<grid, threads, lds, st>>>(a);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+template <int KIND>
+static int launch_expert(int K, int sd, dim3 grid, hipStream_t st, const MoeArgs &a) {
+  const int gpw = expert_gpw(K), threads = 64 * expert_waves(K);
+  if (gpw == 16) return sd == RLQ_F16 ? launch_expert_inst<16, 0, KIND>(grid, threads, st, a)
+                                      : launch_expert_inst<16, 1, KIND>(grid, threads, st, a);
+  return sd == RLQ_F16 ? launch_expert_inst<24, 0, KIND>(grid, threads, st, a)
+                       : launch_expert_inst<24, 1, KIND>(grid, threads, st, a);
+}
+
+static size_t sort_lds_bytes(int E, int wpe) { return (3 * 1024 + 32) * 4 + (size_t)2 * (E + 1) * wpe * 4; }
+static int sort_wpe(int E) { return std::max(1, std::min(32, 8192 / (E + 1))); }
+
+static int check_moe_shape(const char *fn, int T, int E, int topk, int H, int I) {
+  RLQ_REQUIRE(T >= 1 && E >= 1 && E <= kMaxExperts, "%s: T=%d E=%d (1 <= E <= %d)", fn, T, E, kMaxExperts);
+  RLQ_REQUIRE(topk >= 1 && topk <= kMaxTopk && topk <= E, "%s: topk=%d (1..%d, <= E)", fn, topk, kMaxTopk);
+  RLQ_REQUIRE((long long)T * (topk + 1) < (1LL << 30), "%s: T=%d is too large", fn, T);
+  if (H > 0) RLQ_REQUIRE(H % 64 == 0 && H <= 16 * 24 * kGroup, "%s: H=%d must be a multiple of 64 and <= %d", fn, H,
+                         16 * 24 * kGroup);
+  if (I > 0) RLQ_REQUIRE(I % 64 == 0 && I <= 16 * 24 * kGroup, "%s: I=%d must be a multiple of 64 and <= %d", fn, I,
+                         16 * 24 * kGroup);
+  return 0;
+}
+
+}  // namespace rlq
+
+using namespace rlq;
+
+extern "C" {
+
+size_t rlq_moe_max_items(int T, int E, int topk) {
+  if (T < 1 || E < 1 || topk < 1) return 0;
+  return (size_t)moe_max_items(T, E, topk);
+}
+
+int rlq_moe_route(const float *logits, int logit_stride, int T, int E, int topk, int norm_topk, int *sel, float *w,
+                  int *tok, int *inv, int *items, int *n_items, void *stream) {
+  if (int rc = check_moe_shape("rlq_moe_route", T, E, topk, 0, 0)) return rc;
+  RLQ_REQUIRE(logit_stride >= E + 1, "rlq_moe_route: logit_stride=%d < E + 1 = %d", logit_stride, E + 1);
+  RLQ_REQUIRE(logits && sel && w && tok && inv && items && n_items, "rlq_moe_route: null pointer argument");
+  RLQ_REQUIRE(aligned(items, 16), "rlq_moe_route: items must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 g1((T + 3) / 4);
+  const int epl = (E + 63) / 64;
+  if (epl <= 1) moe_topk_kernel<1><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
+  else if (epl <= 2) moe_topk_kernel<2><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
+  else if (epl <= 4) moe_topk_kernel<4><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
+  else if (epl <= 8) moe_topk_kernel<8><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
+  else moe_topk_kernel<16><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
+  RLQ_HIP(hipGetLastError());
+  const int wpe = sort_wpe(E);
+  const size_t lds = sort_lds_bytes(E, wpe);
+  static bool attr_set = false;
+  if (!attr_set) {
+    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_sort_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_set = true;
+  }
+  moe_sort_kernel<<<1, 1024, lds, st>>>(sel, T, E, topk + 1, wpe, tok, inv, reinterpret_cast<int4 *>(items), n_items);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+int rlq_moe_gate_up(const void *x, int x_stride, int T, int H, int I, int E, int topk, const void *packed_gu,
+                    int scale_dtype, const int *tok, const int *items, const int *n_items, void *act, int act_stride,
+                    void *stream) {
+  if (int rc = check_moe_shape("rlq_moe_gate_up", T, E, topk, H, I)) return rc;
+  RLQ_REQUIRE(scale_dtype == RLQ_F16 || scale_dtype == RLQ_BF16, "rlq_moe_gate_up: unknown scale dtype %d", scale_dtype);
+  RLQ_REQUIRE(x && packed_gu && tok && items && n_items && act, "rlq_moe_gate_up: null pointer argument");
+  RLQ_REQUIRE(x_stride >= H && x_stride % 8 == 0 && aligned(x, 16), "rlq_moe_gate_up: x must be 16-byte aligned "
+              "with x_stride >= H and a multiple of 8 (got %d)", x_stride);
+  RLQ_REQUIRE(act_stride >= I && aligned(act, 2), "rlq_moe_gate_up: act_stride=%d < I=%d", act_stride, I);
+  RLQ_REQUIRE((long long)T * x_stride * 2 < (1LL << 31), "rlq_moe_gate_up: x spans more than 2 GiB");
+  RLQ_REQUIRE(aligned(packed_gu, 16) && aligned(items, 16), "rlq_moe_gate_up: packed and items must be 16-byte aligned");
+  const int N = (E + 1) * 2 * I;
+  MoeArgs a;
+  a.x = static_cast<const _Float16 *>(x);
+  a.tok = tok;
+  a.codes = static_cast<const u32x4 *>(packed_gu);
+  a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed_gu) + packed_code_bytes(H, N));
+  a.items = reinterpret_cast<const int4 *>(items);
+  a.n_items = n_items;
+  a.out = act;
+  a.x_rows = T;
+  a.x_stride = x_stride;
+  a.K = H;
+  a.tiles_per_expert = 2 * I / 16;
+  a.out_stride = act_stride;
+  const dim3 grid(a.tiles_per_expert, moe_max_items(T, E, topk));
+  return launch_expert<0>(H, scale_dtype, grid, static_cast<hipStream_t>(stream), a);
+}
+
+int rlq_moe_down(const void *act, int act_stride, int T, int H, int I, int E, int topk, const void *packed_dn,
+                 int scale_dtype, const int *items, const int *n_items, float *y, int y_stride, void *stream) {
+  if (int rc = check_moe_shape("rlq_moe_down", T, E, topk, H, I)) return rc;
+  RLQ_REQUIRE(scale_dtype == RLQ_F16 || scale_dtype == RLQ_BF16, "rlq_moe_down: unknown scale dtype %d", scale_dtype);
+  RLQ_REQUIRE(act && packed_dn && items && n_items && y, "rlq_moe_down: null pointer argument");
+  RLQ_REQUIRE(act_stride >= I && act_stride % 8 == 0 && aligned(act, 16), "rlq_moe_down: act must be 16-byte aligned "
+              "with act_stride >= I and a multiple of 8 (got %d)", act_stride);
+  RLQ_REQUIRE(y_stride >= H, "rlq_moe_down: y_stride=%d < H=%d", y_stride, H);
+  const long long A = (long long)T * (topk + 1);
+  RLQ_REQUIRE(A * act_stride * 2 < (1LL << 31), "rlq_moe_down: act spans more than 2 GiB");
+  RLQ_REQUIRE(aligned(packed_dn, 16) && aligned(items, 16), "rlq_moe_down: packed and items must be 16-byte aligned");
+  const int N = (E + 1) * H;
+  MoeArgs a;
+  a.x = static_cast<const _Float16 *>(act);
+  a.tok = nullptr;
+  a.codes = static_cast<const u32x4 *>(packed_dn);
+  a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed_dn) + packed_code_bytes(I, N));
+  a.items = reinterpret_cast<const int4 *>(items);
+  a.n_items = n_items;
+  a.out = y;
+  a.x_rows = (int)A;
+  a.x_stride = act_stride;
+  a.K = I;
+  a.tiles_per_expert = H / 16;
+  a.out_stride = y_stride;
+  const dim3 grid(a.tiles_per_expert, moe_max_items(T, E, topk));
+  return launch_expert<1>(I, scale_dtype, grid, static_cast<hipStream_t>(stream), a);
+}
+
+int rlq_moe_combine(const float *y, int y_stride, const int *inv, const float *w, int T, int topk, int H, float *h,
+                    int h_stride, void *stream) {
+  RLQ_REQUIRE(T >= 1 && H >= 1 && topk >= 1 && topk <= kMaxTopk, "rlq_moe_combine: T=%d H=%d topk=%d", T, H, topk);
+  RLQ_REQUIRE(y && inv && w && h, "rlq_moe_combine: null pointer argument");
+  RLQ_REQUIRE(y_stride >= H && h_stride >= H, "rlq_moe_combine: strides must be >= H");
+  const dim3 grid((H + 255) / 256, T);
+  moe_combine_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(y, y_stride, inv, w, T, topk + 1, H, h,
+                                                                         h_stride);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+// Workspace of rlq_moe, in order: sel, w, tok, inv [A] (4 bytes each), items [max_items][4]
+// ints, n_items (padded to 16 bytes), act fp16 [A][I], y fp32 [A][H]; each part 256-byte aligned.
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+size_t rlq_moe_workspace_bytes(int T, int E, int topk, int H, int I) {
+  if (T < 1 || E < 1 || topk < 1 || H < 1 || I < 1) return 0;
+  const size_t A = (size_t)T * (topk + 1);
+  return 4 * align256(A * 4) + align256((size_t)moe_max_items(T, E, topk) * 16) + 256 + align256(A * I * 2) +
+         align256(A * H * 4);
+}
+
+int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, int T, int E, int topk, int norm_topk,
+            int H, int I, const void *packed_gu, const void *packed_dn, int scale_dtype, float *h, int h_stride,
+            void *workspace, size_t workspace_bytes, void *stream) {
+  if (int rc = check_moe_shape("rlq_moe", T, E, topk, H, I)) return rc;
+  const size_t need = rlq_moe_workspace_bytes(T, E, topk, H, I);
+  RLQ_REQUIRE(workspace && workspace_bytes >= need, "rlq_moe: workspace of %zu bytes is smaller than the %zu this call "
+              "needs", workspace_bytes, need);
+  RLQ_REQUIRE(aligned(workspace, 256), "rlq_moe: workspace must be 256-byte aligned");
+  const size_t A = (size_t)T * (topk + 1);
+  char *p = static_cast<char *>(workspace);
+  int *sel = reinterpret_cast<int *>(p);            p += align256(A * 4);
+  float *w = reinterpret_cast<float *>(p);          p += align256(A * 4);
+  int *tok = reinterpret_cast<int *>(p);            p += align256(A * 4);
+  int *inv = reinterpret_cast<int *>(p);            p += align256(A * 4);
+  int *items = reinterpret_cast<int *>(p);          p += align256((size_t)moe_max_items(T, E, topk) * 16);
+  int *n_items = reinterpret_cast<int *>(p);        p += 256;
+  _Float16 *act = reinterpret_cast<_Float16 *>(p);  p += align256(A * I * 2);
+  float *y = reinterpret_cast<float *>(p);
+  if (int rc = rlq_moe_route(logits, logit_stride, T, E, topk, norm_topk, sel, w, tok, inv, items, n_items, stream))
+    return rc;
+  if (int rc = rlq_moe_gate_up(x, x_stride, T, H, I, E, topk, packed_gu, scale_dtype, tok, items, n_items, act, I,
+                               stream))
+    return rc;
+  if (int rc = rlq_moe_down(act, I, T, H, I, E, topk, packed_dn, scale_dtype, items, n_items, y, H, stream)) return rc;
+  return rlq_moe_combine(y, H, inv, w, T, topk, H, h, h_stride, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,204 @@
+// The packed 4-bit affine weight layout and the MFMA tile arithmetic shared by the dense
+// decode kernel (linear.hip) and the grouped expert kernels (moe.hip).
+//
+// Packed device layout (made once at upload, from the MLX layout or the .rlm blocked
+// layout; see include/rlq.h), for tiles t of 16 output rows, G = K/64 groups padded to
+// G4 = ceil(G/4) quads, and group pairs p (groups 2p, 2p+1):
+//   codes: 1024 bytes per (t, p) at ((t*2*G4 + p) * 64 + l) * 16: lane l = 16j + c holds
+//          words (8g + 4s + j of row 16t + c) for (g, s) = (2p,0), (2p,1), (2p+1,0), (2p+1,1)
+//          (tools/convert.py:82-89 nibble order);
+//   scale/bias: after the codes, 16 bytes per (t, quad q, row c) at ((t*G4 + q)*16 + c)*16:
+//          s | b << 16 for groups 4q .. 4q+3;
+// rows beyond N and groups beyond G zero. One 16-byte load per lane brings a lane its
+// operands for two groups, and a wave's loads for consecutive group pairs are
+// consecutive kilobytes: a plain stream for the memory system. A stack of matrices whose
+// row counts are multiples of 16 (the experts of a MoE layer) packs as one matrix, and
+// matrix e starts at tile e * rows / 16.
+//
+// Matrix cores: v_mfma_f32_16x16x32_f16 (wave64), A = activations (rows = tokens), B =
+// codes (cols = output features):
+//   A (16 x 32): lane l holds row l%16, k = 8*(l/16) .. +7
+//   B (32 x 16): lane l holds col l%16, k = 8*(l/16) .. +7
+//   D (16 x 16): lane l holds col l%16, rows 4*(l/16) .. +3
+// One group of 64 inputs is two MFMA steps s = 0, 1 (k = 64g + 32s .. +31); lane (c, j) =
+// (l%16, l/16) feeds uint32 word 8g + 4s + j of row c (k = 64g + 32s + 8j .. +7).
+//
+// Operand trick: a uint32 of eight codes becomes four fp16 pairs with five ops,
+//   d0 = u & 0x000F000F -> (q0, q4)          d1 = u & 0x00F000F0 -> (16 q1, 16 q5)
+//   d2 = (u>>8) & 0x000F000F -> (q2, q6)     d3 = (u>>8) & 0x00F000F0 -> (16 q3, 16 q7)
+// each half being the subnormal (code or 16 * code) * 2^-24, exact. The activation
+// operand carries the same element order with the odd elements divided by 16:
+//   (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16),
+// so one MFMA step sums x_e * q_e * 2^-24 over the eight elements. (x/16 is exact unless
+// |x| < 2^-10, where it rounds to the fp16 subnormal grid: an error below 2^-25 * 16 * 15
+// per such element.) The f16 MFMA of gfx950 sums products of subnormal operands with
+// about five bits less precision than normal ones (measured: 3.4e-6 of a group's rms
+// against 1e-7), so only the codes take this fast path: the group sums come from a second
+// MFMA against the normal constant (1, 1, 16, 16, ...), which undoes the 1/16 and lands
+// them in the accumulator layout. Per group, acc += (s * 2^24) * part + b * gsum in fp32
+// (both rescalings exact). An MFMA output row depends only on its own operand row, so a
+// token's result does not depend on which other tokens share the tile.
+#pragma once
+
+#include "rlq_common.h"
+
+namespace rlq {
+
+constexpr int kGroup = 64;
+constexpr int kBufFlags = 0x00020000;             // buffer descriptor word 3 for raw 32-bit accesses
+constexpr int kNonTemporal = 2;                   // buffer load cache policy: stream, do not keep
+constexpr uint32_t kFarOffset = 0x7FFFFFF0u;      // a buffer offset past every range: reads zero
+constexpr float kTwo24 = 16777216.0f;             // undoes the 2^-24 of subnormal code operands
+
+__host__ __device__ inline int tiles_of(int N) { return (N + 15) / 16; }
+__host__ __device__ inline int quads_of(int K) { return (K / kGroup + 3) / 4; }
+inline size_t packed_code_bytes(int K, int N) { return (size_t)tiles_of(N) * quads_of(K) * 2048; }
+inline size_t packed_bytes(int K, int N) { return (size_t)tiles_of(N) * quads_of(K) * 2304; }
+
+// Row order of a packed MoE gate/up stack: the source stack holds, per expert, I gate rows
+// then I up rows ([E][2I][K], tools/quantize.py:168-228); packed tile j of an expert holds
+// gate rows 8j .. 8j+7 then up rows 8j .. 8j+7, so one 16-row tile yields both halves of
+// SwiGLU for 8 features. Returns the source row of packed row n (I % 8 == 0).
+__host__ __device__ inline int gate_up_source_row(int n, int I) {
+  const int e = n / (2 * I), r = n - e * 2 * I, j = r >> 4, c = r & 15;
+  return e * 2 * I + (c < 8 ? 8 * j + c : I + 8 * j + (c - 8));
+}
+
+__device__ __forceinline__ half8 nib8_to_half8_oddx16(uint32_t u) {
+  const uint32_t t = u >> 8;
+  u32x4 d;
+  d[0] = u & 0x000F000Fu;
+  d[1] = u & 0x00F000F0u;
+  d[2] = t & 0x000F000Fu;
+  d[3] = t & 0x00F000F0u;
+  return __builtin_bit_cast(half8, d);
+}
+
+// eight consecutive activations -> operand order (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16)
+__device__ __forceinline__ u32x4 prep_x8(u32x4 p) {
+  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  const half2v sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(p[2], p[0], 0x05040100u);  // (x0, x4)
+  r[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(p[2], p[0], 0x07060302u)) * sixteenth);
+  r[2] = __builtin_amdgcn_perm(p[3], p[1], 0x05040100u);  // (x2, x6)
+  r[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(p[3], p[1], 0x07060302u)) * sixteenth);
+  return r;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kBufFlags);
+}
+
+// acc + float(s16) * p with the 16-bit float taken from the low or high half of a packed pair
+template <int SD, int HI>
+__device__ __forceinline__ float fma_scale(uint32_t pr, float p, float acc) {
+  if constexpr (SD == 0) {
+    const _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)(HI ? (pr >> 16) : (pr & 0xFFFFu)));
+    return __builtin_fmaf(static_cast<float>(v), p, acc);
+  } else {
+    const float v = __uint_as_float(HI ? (pr & 0xFFFF0000u) : (pr << 16));
+    return __builtin_fmaf(v, p, acc);
+  }
+}
+
+// Descriptors over one wave's part of one 16-row tile: groups [wg0, wg0 + GPW) of tile t.
+// Loads past the wave's part (padding groups, the next wave's range) return zeros.
+struct WaveTile {
+  __amdgpu_buffer_rsrc_t rw, rs;
+};
+
+__device__ __forceinline__ WaveTile wave_tile(const u32x4 *codes, const u32x4 *sb, int t, int G4, int wg0, int gpw) {
+  const int wq1 = min(4 * G4, wg0 + gpw);
+  WaveTile w;
+  w.rw = make_rsrc(codes + ((size_t)t * 2 * G4 + wg0 / 2) * 64, (uint32_t)(wq1 - wg0) / 2u * 1024u);
+  w.rs = make_rsrc(sb + ((size_t)t * G4 + wg0 / 4) * 16, (uint32_t)(wq1 - wg0) / 4u * 256u);
+  return w;
+}
+
+// Every code and scale/bias load of the wave's part, issued at once (non-temporal).
+template <int GPW>
+__device__ __forceinline__ void issue_tile_loads(const WaveTile &w, int lane, u32x4 (&wq)[GPW / 2],
+                                                 u32x4 (&sq)[GPW / 4]) {
+#pragma unroll
+  for (int pp = 0; pp < GPW / 2; ++pp)
+    wq[pp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w.rw, 16u * lane, (uint32_t)pp * 1024u, kNonTemporal));
+#pragma unroll
+  for (int qq = 0; qq < GPW / 4; ++qq)
+    sq[qq] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w.rs, 16u * (lane & 15), (uint32_t)qq * 256u, kNonTemporal));
+}
+
+// One group jg of the wave's part: acc[r] += s * (x . q) + b * gsum for the first NACC
+// accumulator rows (NACC = 1 when only token row 0 is live).
+template <int GPW, int SD, int NACC>
+__device__ __forceinline__ void group_step(f32x4 &acc, const half8 (&af)[2], const u32x4 (&wq)[GPW / 2],
+                                           const u32x4 (&sq)[GPW / 4], int jg) {
+  const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x4C004C00u, 0x3C003C00u, 0x4C004C00u});  // 1, 16
+  f32x4 p = {}, gsv = {};
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], nib8_to_half8_oddx16(wq[jg >> 1][2 * (jg & 1) + s]), p, 0, 0, 0);
+    gsv = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, gsv, 0, 0, 0);
+  }
+  const uint32_t pr = sq[jg >> 2][jg & 3];
+  const float sc = fma_scale<SD, 0>(pr, kTwo24, 0.0f);   // s * 2^24, exact: undoes the codes' 2^-24
+#pragma unroll
+  for (int r = 0; r < NACC; ++r) acc[r] = fma_scale<SD, 1>(pr, gsv[r], __builtin_fmaf(sc, p[r], acc[r]));
+}
+
+// The wave's part of a 16-row weight tile times up to 16 token rows whose activations
+// are read straight from memory (L2-resident), two groups ahead, and put in operand order
+// in registers. rx covers the activations; lane (c16, j4) reads its row at byte offset
+// xoff (row start + wave's first element + 16 * j4); lanes of rows that do not exist pass
+// live = false and read zeros. wn = real groups of the wave's part.
+template <int GPW, int SD>
+__device__ __forceinline__ f32x4 tile_dot_rows(const WaveTile &w, __amdgpu_buffer_rsrc_t rx, uint32_t xoff, bool live,
+                                               int wn, int lane) {
+  u32x4 wq[GPW / 2], sq[GPW / 4];
+  auto ldx = [&](int jg, int s) -> u32x4 {
+    const bool ok = live && jg < wn;
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rx, ok ? xoff + (uint32_t)(jg * kGroup + 32 * s) * 2u : kFarOffset, 0, 0));
+  };
+  u32x4 ax[3][2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) ax[d][s] = ldx(d, s);
+  issue_tile_loads<GPW>(w, lane, wq, sq);
+  __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before the first multiply
+  f32x4 acc = {};
+#pragma unroll
+  for (int jg = 0; jg < GPW; ++jg) {
+    if (jg + 2 < GPW) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) ax[(jg + 2) % 3][s] = ldx(jg + 2, s);
+    }
+    const half8 af[2] = {__builtin_bit_cast(half8, prep_x8(ax[jg % 3][0])),
+                         __builtin_bit_cast(half8, prep_x8(ax[jg % 3][1]))};
+    group_step<GPW, SD, 4>(acc, af, wq, sq, jg);
+    // The group's epilogue happens here, not after the last group: without this the
+    // compiler sinks every group's scale/bias FMAs below the last MFMA and keeps all
+    // the partial products alive (register spills).
+    asm volatile("" : "+v"(acc));
+  }
+  return acc;
+}
+
+// Waves 1.. of the workgroup hand their partials to wave 0, which adds them in wave order
+// (a fixed order: the result depends only on the number of waves). red: (waves-1)*64
+// f32x4 of LDS. Returns the total in wave 0 (other waves' return value is unspecified).
+__device__ __forceinline__ f32x4 reduce_waves(f32x4 acc, f32x4 *red, int wave, int waves, int lane) {
+  if (wave > 0) red[(wave - 1) * 64 + lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    for (int w = 1; w < waves; ++w) {
+      const f32x4 o = red[(w - 1) * 64 + lane];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] += o[v];
+    }
+  }
+  return acc;
+}
+
+}  // namespace rlq

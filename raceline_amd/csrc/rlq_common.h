@@ -50,22 +50,29 @@ __device__ __forceinline__ float scale_f32(uint16_t bits) {
   }
 }
 
+// Two fp16 values 1024 + a, 1024 + b (a, b < 1024 integers, as the low bits of each half
+// over the exponent pattern 0x6400) minus 1024: exactly a and b, as normal fp16 numbers.
+// (Codes go to the matrix cores as normal numbers: the f16 MFMA of gfx950 sums products
+// of subnormal operands with about five bits less precision than normal ones.)
+__device__ __forceinline__ uint32_t magic_pair_to_f16(uint32_t bits) {
+  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  const half2v m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, bits | 0x64006400u) + m1024);
+}
+
 // Eight 4-bit codes of one uint32 (element e at bits 4e, tools/convert.py:82-89) -> eight
-// fp16 operands, in element order. Each half's bit pattern is the code itself, i.e. the
-// subnormal q * 2^-24, which is exact; the caller multiplies the scale by 2^24 to undo it.
-// Seven VALU ops for eight weights: two masks, one shift, four byte permutes.
+// fp16 operands q0 .. q7, in element order: two masks, one shift, four byte permutes,
+// four or + packed-add pairs.
 __device__ __forceinline__ half8 nib8_to_half8(uint32_t u) {
   const uint32_t lo = u & 0x0F0F0F0Fu;         // bytes: q0 q2 q4 q6
   const uint32_t hi = (u >> 4) & 0x0F0F0F0Fu;  // bytes: q1 q3 q5 q7
   // perm(S0=hi, S1=lo, sel): selector 0..3 picks bytes of lo, 4..7 bytes of hi, 0x0C a zero byte.
   u32x4 d;
-  d[0] = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u);  // (q0, q1)
-  d[1] = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u);  // (q2, q3)
-  d[2] = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u);  // (q4, q5)
-  d[3] = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u);  // (q6, q7)
+  d[0] = magic_pair_to_f16(__builtin_amdgcn_perm(hi, lo, 0x0C040C00u));  // (q0, q1)
+  d[1] = magic_pair_to_f16(__builtin_amdgcn_perm(hi, lo, 0x0C050C01u));  // (q2, q3)
+  d[2] = magic_pair_to_f16(__builtin_amdgcn_perm(hi, lo, 0x0C060C02u));  // (q4, q5)
+  d[3] = magic_pair_to_f16(__builtin_amdgcn_perm(hi, lo, 0x0C070C03u));  // (q6, q7)
   return __builtin_bit_cast(half8, d);
 }
-
-constexpr float kTwo24 = 16777216.0f;  // undoes the 2^-24 of nib8_to_half8
 
 }  // namespace rlq

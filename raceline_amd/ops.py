@@ -173,3 +173,102 @@ def dequant(pw: PackedWeight, stream=None) -> torch.Tensor:
     out = torch.empty((pw.N, pw.K), dtype=torch.float32, device=pw.packed.device)
     lib.call("rlq_dequant_affine", _ptr(pw.packed), pw.code, pw.K, pw.N, _ptr(out), _stream(stream))
     return out
+
+
+# ------------------------------------------------------------------ mixture of experts
+
+@dataclass
+class MoeWeights:
+    """The expert stacks of one MoE MLP (E routed experts + the shared one, number E):
+    gate_up packed with gate/up rows interleaved per tile (K = H, N = (E+1)*2I) and down
+    packed plainly (K = I, N = (E+1)*H)."""
+    gate_up: PackedWeight
+    down: PackedWeight
+    E: int
+    H: int
+    I: int
+
+
+def pack_moe(gu: tuple, dn: tuple, E: int, H: int, I: int, stream=None) -> MoeWeights:
+    """MLX-layout stacks -> MoeWeights. gu = (w [(E+1)*2I][H/8], s, b [(E+1)*2I][H/64]);
+    dn = (w [(E+1)*H][I/8], s, b [(E+1)*H][I/64])."""
+    gw, gs, gb = gu
+    N, K = _check_mlx(gw, gs, gb)
+    if (N, K) != ((E + 1) * 2 * I, H):
+        raise ValueError(f"gate/up stack is [{N}][{K}], expected [{(E + 1) * 2 * I}][{H}]")
+    out = torch.empty(packed_bytes(H, N), dtype=torch.uint8, device=gw.device)
+    lib.call("rlq_pack_moe_gate_up", _ptr(gw), _ptr(gs), _ptr(gb), H, E + 1, I, _ptr(out), _stream(stream))
+    g = PackedWeight(out, H, N, gs.dtype)
+    d = pack_affine(*dn, stream=stream)
+    if (d.N, d.K) != ((E + 1) * H, I):
+        raise ValueError(f"down stack is [{d.N}][{d.K}], expected [{(E + 1) * H}][{I}]")
+    return MoeWeights(g, d, E, H, I)
+
+
+@dataclass
+class MoeRouting:
+    sel: torch.Tensor       # int32 [T*S]
+    w: torch.Tensor         # float32 [T*S]
+    tok: torch.Tensor       # int32 [T*S]: token of each sorted row
+    inv: torch.Tensor       # int32 [T*S]: sorted row of each assignment
+    items: torch.Tensor     # int32 [max_items][4]
+    n_items: torch.Tensor   # int32 [1]
+    T: int
+    topk: int
+
+
+def moe_route(logits: torch.Tensor, E: int, topk: int, norm_topk: bool = True, stream=None) -> MoeRouting:
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1 or logits.shape[1] < E + 1:
+        raise ValueError("logits must be a row-major float32 [T][>= E+1] matrix")
+    T = logits.shape[0]
+    A = T * (topk + 1)
+    dev = logits.device
+    mi = int(lib.load().rlq_moe_max_items(T, E, topk))
+    r = MoeRouting(torch.empty(A, dtype=torch.int32, device=dev), torch.empty(A, dtype=torch.float32, device=dev),
+                   torch.empty(A, dtype=torch.int32, device=dev), torch.empty(A, dtype=torch.int32, device=dev),
+                   torch.empty((max(mi, 1), 4), dtype=torch.int32, device=dev),
+                   torch.empty(1, dtype=torch.int32, device=dev), T, topk)
+    lib.call("rlq_moe_route", _ptr(logits), logits.stride(0), T, E, topk, 1 if norm_topk else 0, _ptr(r.sel), _ptr(r.w),
+             _ptr(r.tok), _ptr(r.inv), _ptr(r.items), _ptr(r.n_items), _stream(stream))
+    return r
+
+
+def moe_gate_up(x: torch.Tensor, mw: MoeWeights, r: MoeRouting, stream=None) -> torch.Tensor:
+    """act fp16 [T*S][I]: SwiGLU of the routed rows' gate/up products (sorted row order)."""
+    if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < mw.H:
+        raise ValueError("x must be a row-major float16 [T][>= H] matrix")
+    act = torch.empty((r.T * (r.topk + 1), mw.I), dtype=torch.float16, device=x.device)
+    lib.call("rlq_moe_gate_up", _ptr(x), x.stride(0), r.T, mw.H, mw.I, mw.E, r.topk, _ptr(mw.gate_up.packed),
+             mw.gate_up.code, _ptr(r.tok), _ptr(r.items), _ptr(r.n_items), _ptr(act), act.stride(0), _stream(stream))
+    return act
+
+
+def moe_down(act: torch.Tensor, mw: MoeWeights, r: MoeRouting, stream=None) -> torch.Tensor:
+    y = torch.empty((r.T * (r.topk + 1), mw.H), dtype=torch.float32, device=act.device)
+    lib.call("rlq_moe_down", _ptr(act), act.stride(0), r.T, mw.H, mw.I, mw.E, r.topk, _ptr(mw.down.packed),
+             mw.down.code, _ptr(r.items), _ptr(r.n_items), _ptr(y), y.stride(0), _stream(stream))
+    return y
+
+
+def moe_combine(y: torch.Tensor, r: MoeRouting, h: torch.Tensor, stream=None) -> torch.Tensor:
+    lib.call("rlq_moe_combine", _ptr(y), y.stride(0), _ptr(r.inv), _ptr(r.w), r.T, r.topk, h.shape[1], _ptr(h),
+             h.stride(0), _stream(stream))
+    return h
+
+
+def moe_workspace_bytes(T: int, E: int, topk: int, H: int, I: int) -> int:
+    return int(lib.load().rlq_moe_workspace_bytes(T, E, topk, H, I))
+
+
+def moe(x: torch.Tensor, logits: torch.Tensor, mw: MoeWeights, topk: int, h: torch.Tensor, norm_topk: bool = True,
+        workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """h[t] += the MoE MLP of x[t] (route, gate/up + SwiGLU, down, combine), in one call."""
+    T = x.shape[0]
+    if h.dtype != torch.float32 or h.stride(1) != 1 or h.shape[0] < T or h.shape[1] < mw.H:
+        raise ValueError("h must be a row-major float32 [T][>= H] matrix")
+    nbytes = moe_workspace_bytes(T, mw.E, topk, mw.H, mw.I)
+    ws = workspace if workspace is not None else torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    lib.call("rlq_moe", _ptr(x), x.stride(0), _ptr(logits), logits.stride(0), T, mw.E, topk, 1 if norm_topk else 0,
+             mw.H, mw.I, _ptr(mw.gate_up.packed), _ptr(mw.down.packed), mw.gate_up.code, _ptr(h), h.stride(0), _ptr(ws),
+             ws.numel(), _stream(stream))
+    return h

@@ -32,6 +32,9 @@ extern "C" {
 #endif
 
 enum { RLQ_F16 = 0, RLQ_BF16 = 1 };  /* 16-bit float type of scales and biases */
+/* Codebooks of the native 4-bit format (tools/quantlib.py:23-28): two's complement -8..7,
+ * the same plus 0.5, and fp4 e2m1. */
+enum { RLQ_BOOK_INT15 = 1, RLQ_BOOK_INT16 = 2, RLQ_BOOK_FP4 = 3 };
 
 /* ---------------------------------------------------------------- library */
 
@@ -99,6 +102,34 @@ int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int
                              const void *packed, int scale_dtype,
                              float *y, int y_stride, int accum,
                              void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------- native 4-bit linear */
+
+/* The native ("q4n") format: a 4-bit codebook value per weight, one fp32 scale per output
+ * row and one per input column, W[n][k] = L[q[n][k]] * s[n] * c[k] (tools/quantlib.py:62-64,
+ * tools/convert.py:197-216). The column scale is folded into the activations by whichever
+ * kernel produces them (src/engine.mm:515-530), as in the reference; the kernels apply s.
+ * Codes are packed into the same tile layout as the affine codes, without the scale/bias
+ * section: rlq_packed_codes_bytes(K, N) = T*G4*2048 bytes. */
+size_t rlq_packed_codes_bytes(int K, int N);
+
+/* Row-major codes, uint32 [N][K/8] with element k at bits 4*(k%8) -> packed codes. */
+int rlq_pack_codes(const uint32_t *w, int K, int N, void *packed, void *stream);
+
+/* Blocked q4n file layout (bytes [n_pad/256][K][128], tools/convert.py:197-216) rows
+ * [row0, row0+rows) -> packed codes. */
+int rlq_pack_native_blocked(const uint8_t *w_blk, int K, int n_pad, int row0, int rows, void *packed, void *stream);
+
+/* y[m][n] (+)= s_row[n] * sum_k x[m][k] * L[q[n][k]]  (+ 0.5 * sum_k x[m][k] inside the row
+ * scale for RLQ_BOOK_INT16). Replaces linear_q4n (kernels/linear.metal:118-184). x fp16
+ * [M][x_stride] (column scale already applied); s_row fp32 [N]; y fp32 [M][y_stride]. The
+ * workspace (rlq_linear_workspace_bytes) is used by M > 8 with RLQ_BOOK_INT16 only. */
+int rlq_linear_native(const void *x, int x_stride, int M, int K, int N, const void *packed, const float *s_row,
+                      int book, float *y, int y_stride, int accum, void *workspace, size_t workspace_bytes,
+                      void *stream);
+int rlq_linear_native_kernel(int kernel, const void *x, int x_stride, int M, int K, int N, const void *packed,
+                             const float *s_row, int book, float *y, int y_stride, int accum, void *workspace,
+                             size_t workspace_bytes, void *stream);
 
 /* gsum[m][g] = sum_{k<64} x[m][64g+k], summed in order in fp32 (kernels/linear.metal:34-45). */
 int rlq_group_sums(const void *x, int x_stride, int M, int K, float *gsum, void *stream);

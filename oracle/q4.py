@@ -25,7 +25,8 @@ __all__ = [
     "quantize_affine_rtn", "dequant_affine", "dequant_native",
     "group_sums", "linear_affine_f64", "linear_affine_factored_f64", "linear_affine_cpu_f32",
     "linear_native_f64", "check_close", "rel_err",
-    "XorShift64", "reference_test_case", "REFERENCE_TEST_CASES",
+    "XorShift64", "reference_test_case", "REFERENCE_TEST_CASES", "reference_native_case",
+    "REFERENCE_NATIVE_CASES",
 ]
 
 
@@ -451,6 +452,22 @@ def reference_test_case(M: int, K: int, N: int, gen: XorShift64 | None = None):
     x = XorShift64.uniform_of(gen.stream(M * K), -2.0, 2.0).astype(np.float16).reshape(M, K)
     return q, s.reshape(N, G), b.reshape(N, G), x
 
+
+def reference_native_case(M: int, K: int, N: int, gen: XorShift64 | None = None):
+    """The inputs of one native-format case of tests/test_linear.mm (check_native, :316-350),
+    drawn as make_native(keep_ref) (:252-266) and make_input (:141-147) draw them: row
+    scales U(0.002, 0.02) for each of the N rows, then codes rnd() & 15 row-major [N][K],
+    then activations fp16(U(-2, 2)) [M][K]. Returns (codes uint8 [N][K], s float32 [N],
+    x float16 [M][K])."""
+    gen = gen or XorShift64()
+    s = XorShift64.uniform_of(gen.stream(N), 0.002, 0.02).astype(np.float32)
+    q = (gen.stream(N * K) & np.uint64(15)).astype(np.uint8).reshape(N, K)
+    x = XorShift64.uniform_of(gen.stream(M * K), -2.0, 2.0).astype(np.float16).reshape(M, K)
+    return q, s, x
+
+
+# The native cases of tests/test_linear.mm:447-450 (each for every codebook) as (M, K, N).
+REFERENCE_NATIVE_CASES = [(1, 2560, 9216), (40, 2560, 1000), (70, 9216, 2560)]
 
 # The correctness cases of tests/test_linear.mm:440-446 as (M, K, N).
 REFERENCE_TEST_CASES = [(1, 2560, 9216), (5, 2560, 9216), (40, 2560, 9216), (70, 2560, 9216),

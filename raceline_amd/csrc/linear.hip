@@ -45,7 +45,7 @@ __global__ void pack_mlx_kernel(const uint32_t *w, const uint16_t *s, const uint
     }
   }
   codes[i] = v;
-  if (j == 0 && (p & 1) == 0) {
+  if (sb != nullptr && j == 0 && (p & 1) == 0) {   // sb == nullptr: a codes-only (native) matrix
     const int q = p >> 1;
     u32x4 e4 = {};
     if (n < N) {
@@ -88,7 +88,7 @@ __global__ void pack_blocked_kernel(const uint8_t *w_blk, const uint16_t *s_blk,
     }
   }
   codes[i] = v;
-  if (j == 0 && (p & 1) == 0) {
+  if (sb != nullptr && j == 0 && (p & 1) == 0) {   // sb == nullptr: a codes-only (native) matrix
     const int q = p >> 1;
     u32x4 e4 = {};
     if (r < rows) {
@@ -186,7 +186,8 @@ constexpr int kGemvMaxM = 8;
 struct GemvArgs {
   const _Float16 *x;
   const u32x4 *codes;
-  const u32x4 *sb;
+  const u32x4 *sb;      // affine: scale/bias quads
+  const float *srow;    // native books: the scale of each output row
   float *y;
   int x_stride, M, K, N, y_stride;
 };
@@ -202,7 +203,8 @@ static size_t gemv_lds_bytes(int M, int waves, int gpw) {
 }
 
 // MAXM: 1 (single-token decode: one activation row, one live accumulator) or 8.
-template <int MAXM, int GPW, int SD, bool ACC>
+// BOOK: kAffine (per-group scale and bias) or a native codebook (one scale per row).
+template <int MAXM, int GPW, int SD, bool ACC, int BOOK>
 __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int waves = blockDim.x >> 6;
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
   const uint32_t xrange = wn > 0 ? (uint32_t)((M - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
 
-  f32x4 acc = {};
+  f32x4 acc = {}, asum = {};
   if constexpr (MAXM == 1) {
     // One token: the wave's activation row is loaded first (the loads complete in issue
     // order, so waiting for it does not wait for the weights), then every weight load is
@@ -240,12 +242,12 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
       const bool in_range = chunk < XCH && (chunk >> 3) < wn;
       xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, in_range ? 16u * chunk : kFarOffset, 0, 0));
     }
-    issue_tile_loads<GPW>(wt, lane, wq, sq);
+    issue_tile_loads<GPW, BOOK>(wt, lane, wq, sq);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < XPER; ++i) {
       const int chunk = lane + 64 * i;
-      if (chunk < XCH) *reinterpret_cast<u32x4 *>(xs + 8 * chunk) = prep_x8(xr[i]);
+      if (chunk < XCH) *reinterpret_cast<u32x4 *>(xs + 8 * chunk) = prep_act<BOOK>(xr[i]);
     }
     // other lanes of this wave read what was just written: keep the LDS reads after the writes
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -262,24 +264,26 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) an[s] = *reinterpret_cast<const half8 *>(xa + (jg + 1) * kGroup + 32 * s);
       }
-      group_step<GPW, SD, 1>(acc, af, wq, sq, jg);
+      book_step<GPW, SD, 1, BOOK>(acc, asum, af, wq, sq, jg);
       __builtin_amdgcn_sched_barrier(0);   // one group at a time: bounded register use
     }
+    if constexpr (BOOK == kInt16) acc[0] = __builtin_fmaf(0.5f, asum[0], acc[0]);
   } else {
     // Several tokens: lane (c16, j4) reads token row c16's activations from memory;
     // rows >= M read zeros.
-    acc = tile_dot_rows<GPW, SD>(wt, rx, (uint32_t)c16 * a.x_stride * 2u + 16u * j4, c16 < M, wn, lane);
+    acc = tile_dot_rows<GPW, SD, BOOK>(wt, rx, (uint32_t)c16 * a.x_stride * 2u + 16u * j4, c16 < M, wn, lane);
   }
 
   // lane (c16, j4) holds token rows 4 j4 .. 4 j4 + 3 of output n
   acc = reduce_waves(acc, red, wave, waves, lane);
   if (wave == 0 && n < a.N && 4 * j4 < M) {
+    const float rs = BOOK == kAffine ? 1.0f : a.srow[n];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = 4 * j4 + v;
       if (m < M) {
         float *dst = a.y + (size_t)m * a.y_stride + n;
-        const float val = acc[v];
+        const float val = BOOK == kAffine ? acc[v] : rs * acc[v];
         *dst = ACC ? *dst + val : val;
       }
     }
@@ -288,29 +292,44 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
 
 static size_t gemv_workspace(int, int, int) { return 0; }
 
-template <int MAXM, int GPW, int SD, bool ACC>
+template <int MAXM, int GPW, int SD, bool ACC, int BOOK>
 static int launch_gemv_inst(dim3 grid, int threads, size_t lds, hipStream_t st, const GemvArgs &a) {
   static bool attr_set = false;  // once per instance, before its first launch
   if (!attr_set) {
-    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4a_kernel<MAXM, GPW, SD, ACC>),
+    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4a_kernel<MAXM, GPW, SD, ACC, BOOK>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr_set = true;
   }
-  gemv_q4a_kernel<MAXM, GPW, SD, ACC><<<grid, threads, lds, st>>>(a);
+  gemv_q4a_kernel<MAXM, GPW, SD, ACC, BOOK><<<grid, threads, lds, st>>>(a);
   return 0;
 }
 
-template <int MAXM, int GPW>
-static int launch_gemv(int sd, int accum, dim3 grid, int threads, size_t lds, hipStream_t st, const GemvArgs &a) {
-  if (sd == RLQ_F16)
-    return accum ? launch_gemv_inst<MAXM, GPW, 0, true>(grid, threads, lds, st, a)
-                 : launch_gemv_inst<MAXM, GPW, 0, false>(grid, threads, lds, st, a);
-  return accum ? launch_gemv_inst<MAXM, GPW, 1, true>(grid, threads, lds, st, a)
-               : launch_gemv_inst<MAXM, GPW, 1, false>(grid, threads, lds, st, a);
+template <int MAXM, int GPW, int BOOK>
+static int launch_gemv_acc(int sd, int accum, dim3 grid, int threads, size_t lds, hipStream_t st, const GemvArgs &a) {
+  if constexpr (BOOK == kAffine) {
+    if (sd == RLQ_BF16)
+      return accum ? launch_gemv_inst<MAXM, GPW, 1, true, BOOK>(grid, threads, lds, st, a)
+                   : launch_gemv_inst<MAXM, GPW, 1, false, BOOK>(grid, threads, lds, st, a);
+  }
+  return accum ? launch_gemv_inst<MAXM, GPW, 0, true, BOOK>(grid, threads, lds, st, a)
+               : launch_gemv_inst<MAXM, GPW, 0, false, BOOK>(grid, threads, lds, st, a);
 }
 
-static int run_gemv(const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd, float *y,
-                    int y_stride, int accum, void *, size_t, hipStream_t st) {
+template <int MAXM, int GPW>
+static int launch_gemv(int book, int sd, int accum, dim3 grid, int threads, size_t lds, hipStream_t st,
+                       const GemvArgs &a) {
+  switch (book) {
+    case kInt15: return launch_gemv_acc<MAXM, GPW, kInt15>(sd, accum, grid, threads, lds, st, a);
+    case kInt16: return launch_gemv_acc<MAXM, GPW, kInt16>(sd, accum, grid, threads, lds, st, a);
+    case kFp4: return launch_gemv_acc<MAXM, GPW, kFp4>(sd, accum, grid, threads, lds, st, a);
+    default: return launch_gemv_acc<MAXM, GPW, kAffine>(sd, accum, grid, threads, lds, st, a);
+  }
+}
+
+// book: kAffine (packed holds codes then scale/bias quads; sd their dtype) or a native
+// codebook (packed holds codes only; srow the row scales).
+static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
+                    const float *srow, float *y, int y_stride, int accum, hipStream_t st) {
   RLQ_REQUIRE(M <= kGemvMaxM, "decode kernel handles M <= %d rows (got %d)", kGemvMaxM, M);
   const int gpw = gemv_gpw(K), waves = gemv_waves(K);
   RLQ_REQUIRE(waves <= 16, "decode kernel: K=%d is larger than the %d it supports", K, 16 * 24 * kGroup);
@@ -319,15 +338,16 @@ static int run_gemv(const _Float16 *x, int x_stride, int M, int K, int N, const 
   a.x = x;
   a.codes = static_cast<const u32x4 *>(packed);
   a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
+  a.srow = srow;
   a.y = y;
   a.x_stride = x_stride; a.M = M; a.K = K; a.N = N; a.y_stride = y_stride;
   const dim3 grid(tiles_of(N));
   const int threads = 64 * waves;
   int rc;
-  if (M == 1) rc = gpw == 16 ? launch_gemv<1, 16>(sd, accum, grid, threads, lds, st, a)
-                             : launch_gemv<1, 24>(sd, accum, grid, threads, lds, st, a);
-  else rc = gpw == 16 ? launch_gemv<kGemvMaxM, 16>(sd, accum, grid, threads, lds, st, a)
-                      : launch_gemv<kGemvMaxM, 24>(sd, accum, grid, threads, lds, st, a);
+  if (M == 1) rc = gpw == 16 ? launch_gemv<1, 16>(book, sd, accum, grid, threads, lds, st, a)
+                             : launch_gemv<1, 24>(book, sd, accum, grid, threads, lds, st, a);
+  else rc = gpw == 16 ? launch_gemv<kGemvMaxM, 16>(book, sd, accum, grid, threads, lds, st, a)
+                      : launch_gemv<kGemvMaxM, 24>(book, sd, accum, grid, threads, lds, st, a);
   if (rc) return rc;
   RLQ_HIP(hipGetLastError());
   return 0;
@@ -365,15 +385,17 @@ __global__ void group_sums_kernel(const _Float16 *x, int x_stride, int M, int K,
 struct GemmArgs {
   const _Float16 *x;
   const u32x4 *codes;
-  const u32x4 *sb;
-  const float *gsT;  // [G][m_pad]
+  const u32x4 *sb;      // affine: scale/bias quads
+  const float *gsT;     // affine: group sums [G][m_pad]
+  const float *srow;    // native books: row scales [N]
+  const float *asum;    // kInt16: activation row sums [m_pad]
   float *y;
   int x_stride, M, K, N, y_stride, m_pad;
 };
 
 constexpr int kBM = 128, kBN = 128, kLdsRow = 128 + 8;
 
-template <int SD, bool ACC>
+template <int SD, bool ACC, int BOOK>
 __global__ __launch_bounds__(256) void gemm_q4a_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 As[kBM * kLdsRow];
 
@@ -414,7 +436,7 @@ __global__ __launch_bounds__(256) void gemm_q4a_kernel(GemmArgs a) {
 #pragma unroll
     for (int ft = 0; ft < 4; ++ft) {
       wq[ft] = tval[ft] ? a.codes[((size_t)tile[ft] * GP + p) * 64 + lane] : u32x4{};
-      sq[ft] = tval[ft] ? a.sb[((size_t)tile[ft] * G4 + (p >> 1)) * 16 + c16] : u32x4{};
+      if constexpr (BOOK == kAffine) sq[ft] = tval[ft] ? a.sb[((size_t)tile[ft] * G4 + (p >> 1)) * 16 + c16] : u32x4{};
     }
     __syncthreads();
 
@@ -426,13 +448,22 @@ __global__ __launch_bounds__(256) void gemm_q4a_kernel(GemmArgs a) {
 #pragma unroll
       for (int ft = 0; ft < 4; ++ft)
 #pragma unroll
-        for (int s = 0; s < 2; ++s) bf[ft][s] = nib8_to_half8(wq[ft][2 * gg + s]);
+        for (int s = 0; s < 2; ++s)
+          bf[ft][s] = BOOK == kAffine ? nib8_to_half8(wq[ft][2 * gg + s]) : native8_to_half8<BOOK>(wq[ft][2 * gg + s]);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         half8 af[2];
         const _Float16 *arow = As + (wm * 64 + mt * 16 + c16) * kLdsRow + 64 * gg + 8 * j4;
 #pragma unroll
         for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(arow + 32 * s);
+        if constexpr (BOOK != kAffine) {
+          // native: one MFMA chain over all of K, the row scale at the end
+#pragma unroll
+          for (int ft = 0; ft < 4; ++ft)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) acc[mt][ft] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bf[ft][s], acc[mt][ft], 0, 0, 0);
+          continue;
+        }
         const f32x4 gq = *reinterpret_cast<const f32x4 *>(a.gsT + (size_t)g * a.m_pad + m0 + wm * 64 + mt * 16 + 4 * j4);
 #pragma unroll
         for (int ft = 0; ft < 4; ++ft) {
@@ -456,46 +487,83 @@ __global__ __launch_bounds__(256) void gemm_q4a_kernel(GemmArgs a) {
     for (int ft = 0; ft < 4; ++ft) {
       const int n = 16 * tile[ft] + c16;
       if (n >= a.N) continue;
+      const float rs = BOOK == kAffine ? 1.0f : a.srow[n];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + wm * 64 + mt * 16 + 4 * j4 + r;
         if (m < a.M) {
+          float v = acc[mt][ft][r];
+          if constexpr (BOOK == kInt16) v = __builtin_fmaf(0.5f, a.asum[m], v);
+          if constexpr (BOOK != kAffine) v *= rs;
           float *dst = a.y + (size_t)m * a.y_stride + n;
-          *dst = ACC ? *dst + acc[mt][ft][r] : acc[mt][ft][r];
+          *dst = ACC ? *dst + v : v;
         }
       }
     }
 }
 
-static size_t gemm_workspace(int M, int K) {
-  const int m_pad = (M + kBM - 1) / kBM * kBM;
-  return (size_t)(K / kGroup) * m_pad * sizeof(float);   // group sums, transposed
+// asum[m] = sum over g of gsT[g][m], in order: the activation row sums the half-step
+// codebook needs.
+__global__ void row_sums_kernel(const float *gsT, int G, int m_pad, int M, float *asum) {
+  const int m = blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  float s = 0.0f;
+  for (int g = 0; g < G; ++g) s += gsT[(size_t)g * m_pad + m];
+  asum[m] = s;
 }
 
-static int run_gemm(const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd, float *y,
-                    int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st) {
-  const size_t need = gemm_workspace(M, K);
-  RLQ_REQUIRE(ws_bytes >= need, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
-  RLQ_REQUIRE(aligned(ws, 16), "workspace must be 16-byte aligned");
+// group sums transposed [G][m_pad], then the row sums [m_pad] (kInt16)
+static size_t gemm_workspace(int M, int K) {
   const int m_pad = (M + kBM - 1) / kBM * kBM;
-  float *gsT = static_cast<float *>(ws);
-  // rows M..m_pad of gsT only feed output rows that are never stored
+  return (size_t)(K / kGroup + 1) * m_pad * sizeof(float);
+}
+
+template <int BOOK>
+static int launch_gemm_book(int sd, int accum, dim3 grid, hipStream_t st, const GemmArgs &a) {
+  if constexpr (BOOK == kAffine) {
+    if (sd == RLQ_BF16) {
+      if (accum) gemm_q4a_kernel<1, true, BOOK><<<grid, 256, 0, st>>>(a);
+      else gemm_q4a_kernel<1, false, BOOK><<<grid, 256, 0, st>>>(a);
+      return 0;
+    }
+  }
+  if (accum) gemm_q4a_kernel<0, true, BOOK><<<grid, 256, 0, st>>>(a);
+  else gemm_q4a_kernel<0, false, BOOK><<<grid, 256, 0, st>>>(a);
+  return 0;
+}
+
+static int run_gemm(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
+                    const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st) {
+  const int m_pad = (M + kBM - 1) / kBM * kBM;
   const int G = K / kGroup;
-  group_sums_kernel<<<(M * G + 255) / 256, 256, 0, st>>>(x, x_stride, M, K, nullptr, gsT, m_pad);
-  RLQ_HIP(hipGetLastError());
   GemmArgs a;
   a.x = x;
   a.codes = static_cast<const u32x4 *>(packed);
   a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
-  a.gsT = gsT; a.y = y;
+  a.gsT = nullptr; a.srow = srow; a.asum = nullptr; a.y = y;
   a.x_stride = x_stride; a.M = M; a.K = K; a.N = N; a.y_stride = y_stride; a.m_pad = m_pad;
+  if (book == kAffine || book == kInt16) {
+    const size_t need = gemm_workspace(M, K);
+    RLQ_REQUIRE(ws_bytes >= need, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
+    RLQ_REQUIRE(aligned(ws, 16), "workspace must be 16-byte aligned");
+    float *gsT = static_cast<float *>(ws);
+    // rows M..m_pad of gsT only feed output rows that are never stored
+    group_sums_kernel<<<(M * G + 255) / 256, 256, 0, st>>>(x, x_stride, M, K, nullptr, gsT, m_pad);
+    RLQ_HIP(hipGetLastError());
+    a.gsT = gsT;
+    if (book == kInt16) {
+      float *asum = gsT + (size_t)G * m_pad;
+      row_sums_kernel<<<(M + 255) / 256, 256, 0, st>>>(gsT, G, m_pad, M, asum);
+      RLQ_HIP(hipGetLastError());
+      a.asum = asum;
+    }
+  }
   const dim3 grid((N + kBN - 1) / kBN, m_pad / kBM);
-  if (sd == RLQ_F16) {
-    if (accum) gemm_q4a_kernel<0, true><<<grid, 256, 0, st>>>(a);
-    else gemm_q4a_kernel<0, false><<<grid, 256, 0, st>>>(a);
-  } else {
-    if (accum) gemm_q4a_kernel<1, true><<<grid, 256, 0, st>>>(a);
-    else gemm_q4a_kernel<1, false><<<grid, 256, 0, st>>>(a);
+  switch (book) {
+    case kInt15: launch_gemm_book<kInt15>(sd, accum, grid, st, a); break;
+    case kInt16: launch_gemm_book<kInt16>(sd, accum, grid, st, a); break;
+    case kFp4: launch_gemm_book<kFp4>(sd, accum, grid, st, a); break;
+    default: launch_gemm_book<kAffine>(sd, accum, grid, st, a); break;
   }
   RLQ_HIP(hipGetLastError());
   return 0;
@@ -571,6 +639,62 @@ int rlq_pack_affine_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const u
   return 0;
 }
 
+size_t rlq_packed_codes_bytes(int K, int N) {
+  if (K <= 0 || N <= 0 || K % kGroup) return 0;
+  return packed_code_bytes(K, N);
+}
+
+int rlq_pack_codes(const uint32_t *w, int K, int N, void *packed, void *stream) {
+  RLQ_REQUIRE(N >= 1 && K >= kGroup && K % kGroup == 0, "rlq_pack_codes: bad sizes K=%d N=%d", K, N);
+  RLQ_REQUIRE(N <= 16 * kMaxTiles, "rlq_pack_codes: N=%d exceeds the supported %d", N, 16 * kMaxTiles);
+  RLQ_REQUIRE(w && packed, "rlq_pack_codes: null pointer argument");
+  RLQ_REQUIRE(aligned(w, 4) && aligned(packed, 16), "rlq_pack_codes: misaligned w or packed");
+  const size_t pieces = (size_t)tiles_of(N) * 2 * quads_of(K) * 64;
+  pack_mlx_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      w, nullptr, nullptr, K, N, 0, static_cast<u32x4 *>(packed), nullptr);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+int rlq_pack_native_blocked(const uint8_t *w_blk, int K, int n_pad, int row0, int rows, void *packed, void *stream) {
+  RLQ_REQUIRE(K >= kGroup && K % kGroup == 0, "rlq_pack_native_blocked: K=%d is not a multiple of 64", K);
+  RLQ_REQUIRE(n_pad % 256 == 0 && n_pad > 0, "rlq_pack_native_blocked: n_pad=%d is not a multiple of the block 256",
+              n_pad);
+  RLQ_REQUIRE(row0 >= 0 && rows >= 1 && row0 + rows <= n_pad, "rlq_pack_native_blocked: rows [%d, %d) outside [0, %d)",
+              row0, row0 + rows, n_pad);
+  RLQ_REQUIRE(w_blk && packed, "rlq_pack_native_blocked: null pointer argument");
+  RLQ_REQUIRE(aligned(packed, 16), "rlq_pack_native_blocked: packed must be 16-byte aligned");
+  const size_t pieces = (size_t)tiles_of(rows) * 2 * quads_of(K) * 64;
+  pack_blocked_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      w_blk, nullptr, nullptr, K, row0, rows, static_cast<u32x4 *>(packed), nullptr);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+int rlq_linear_native_kernel(int kernel, const void *x, int x_stride, int M, int K, int N, const void *packed,
+                             const float *s_row, int book, float *y, int y_stride, int accum, void *workspace,
+                             size_t workspace_bytes, void *stream) {
+  int rc = check_linear_args("rlq_linear_native", x, x_stride, M, K, N, packed, RLQ_F16, y, y_stride);
+  if (rc) return rc;
+  RLQ_REQUIRE(book == RLQ_BOOK_INT15 || book == RLQ_BOOK_INT16 || book == RLQ_BOOK_FP4,
+              "rlq_linear_native: unknown codebook %d", book);
+  RLQ_REQUIRE(s_row && aligned(s_row, 4), "rlq_linear_native: null or misaligned row scales");
+  RLQ_REQUIRE(kernel >= 0 && kernel <= 2, "rlq_linear_native_kernel: unknown kernel %d", kernel);
+  const bool gemv = kernel == 1 || (kernel == 0 && M <= kGemvMaxM);
+  auto st = static_cast<hipStream_t>(stream);
+  auto xh = static_cast<const _Float16 *>(x);
+  if (gemv) return run_gemv(book, xh, x_stride, M, K, N, packed, RLQ_F16, s_row, y, y_stride, accum, st);
+  return run_gemm(book, xh, x_stride, M, K, N, packed, RLQ_F16, s_row, y, y_stride, accum, workspace, workspace_bytes,
+                  st);
+}
+
+int rlq_linear_native(const void *x, int x_stride, int M, int K, int N, const void *packed, const float *s_row,
+                      int book, float *y, int y_stride, int accum, void *workspace, size_t workspace_bytes,
+                      void *stream) {
+  return rlq_linear_native_kernel(0, x, x_stride, M, K, N, packed, s_row, book, y, y_stride, accum, workspace,
+                                  workspace_bytes, stream);
+}
+
 size_t rlq_linear_workspace_bytes(int M, int K, int N) {
   if (M <= 0 || K <= 0 || N <= 0 || K % kGroup) return 0;
   return std::max(M <= kGemvMaxM ? gemv_workspace(M, K, N) : (size_t)0, gemm_workspace(M, K));
@@ -585,8 +709,9 @@ int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int
   const bool gemv = kernel == 1 || (kernel == 0 && M <= kGemvMaxM);
   auto st = static_cast<hipStream_t>(stream);
   auto xh = static_cast<const _Float16 *>(x);
-  if (gemv) return run_gemv(xh, x_stride, M, K, N, packed, scale_dtype, y, y_stride, accum, workspace, workspace_bytes, st);
-  return run_gemm(xh, x_stride, M, K, N, packed, scale_dtype, y, y_stride, accum, workspace, workspace_bytes, st);
+  if (gemv) return run_gemv(kAffine, xh, x_stride, M, K, N, packed, scale_dtype, nullptr, y, y_stride, accum, st);
+  return run_gemm(kAffine, xh, x_stride, M, K, N, packed, scale_dtype, nullptr, y, y_stride, accum, workspace,
+                  workspace_bytes, st);
 }
 
 int rlq_linear_affine(const void *x, int x_stride, int M, int K, int N, const void *packed, int scale_dtype, float *y,

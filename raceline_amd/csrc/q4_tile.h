@@ -116,17 +116,42 @@ __device__ __forceinline__ WaveTile wave_tile(const u32x4 *codes, const u32x4 *s
   return w;
 }
 
-// Every code and scale/bias load of the wave's part, issued at once (non-temporal).
-template <int GPW>
+// Every code load of the wave's part and (affine) every scale/bias load, issued at once
+// (non-temporal).
+template <int GPW, int BOOK = kAffine>
 __device__ __forceinline__ void issue_tile_loads(const WaveTile &w, int lane, u32x4 (&wq)[GPW / 2],
                                                  u32x4 (&sq)[GPW / 4]) {
 #pragma unroll
   for (int pp = 0; pp < GPW / 2; ++pp)
     wq[pp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w.rw, 16u * lane, (uint32_t)pp * 1024u, kNonTemporal));
+  if constexpr (BOOK == kAffine) {
 #pragma unroll
-  for (int qq = 0; qq < GPW / 4; ++qq)
-    sq[qq] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w.rs, 16u * (lane & 15), (uint32_t)qq * 256u, kNonTemporal));
+    for (int qq = 0; qq < GPW / 4; ++qq)
+      sq[qq] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w.rs, 16u * (lane & 15), (uint32_t)qq * 256u, kNonTemporal));
+  }
 }
+
+// Activations -> operand order: the affine path's permuted order (prep_x8); native books
+// take the natural order.
+template <int BOOK>
+__device__ __forceinline__ u32x4 prep_act(u32x4 v) {
+  if constexpr (BOOK == kAffine) return prep_x8(v);
+  else return v;
+}
+
+// One group of a native-book tile: the products chain straight into the accumulator (no
+// per-group scale); kInt16 also chains the activation sums (for its +0.5 levels).
+template <int GPW, int BOOK>
+__device__ __forceinline__ void native_step(f32x4 &acc, f32x4 &asum, const half8 (&af)[2], const u32x4 (&wq)[GPW / 2],
+                                            int jg) {
+  const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq[jg >> 1][2 * (jg & 1) + s]), acc, 0, 0, 0);
+    if constexpr (BOOK == kInt16) asum = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, asum, 0, 0, 0);
+  }
+}
+
 
 // One group jg of the wave's part: acc[r] += s * (x . q) + b * gsum for the first NACC
 // accumulator rows (NACC = 1 when only token row 0 is live).
@@ -146,12 +171,22 @@ __device__ __forceinline__ void group_step(f32x4 &acc, const half8 (&af)[2], con
   for (int r = 0; r < NACC; ++r) acc[r] = fma_scale<SD, 1>(pr, gsv[r], __builtin_fmaf(sc, p[r], acc[r]));
 }
 
+// The per-group step of any book: affine (group_step, scales applied per group) or native.
+template <int GPW, int SD, int NACC, int BOOK>
+__device__ __forceinline__ void book_step(f32x4 &acc, f32x4 &asum, const half8 (&af)[2], const u32x4 (&wq)[GPW / 2],
+                                          const u32x4 (&sq)[GPW / 4], int jg) {
+  if constexpr (BOOK == kAffine) group_step<GPW, SD, NACC>(acc, af, wq, sq, jg);
+  else native_step<GPW, BOOK>(acc, asum, af, wq, jg);
+}
+
 // The wave's part of a 16-row weight tile times up to 16 token rows whose activations
 // are read straight from memory (L2-resident), two groups ahead, and put in operand order
 // in registers. rx covers the activations; lane (c16, j4) reads its row at byte offset
 // xoff (row start + wave's first element + 16 * j4); lanes of rows that do not exist pass
 // live = false and read zeros. wn = real groups of the wave's part.
-template <int GPW, int SD>
+// For native books the returned total already includes 0.5 * asum (kInt16); the row
+// scale is the caller's.
+template <int GPW, int SD, int BOOK = kAffine>
 __device__ __forceinline__ f32x4 tile_dot_rows(const WaveTile &w, __amdgpu_buffer_rsrc_t rx, uint32_t xoff, bool live,
                                                int wn, int lane) {
   u32x4 wq[GPW / 2], sq[GPW / 4];
@@ -165,22 +200,26 @@ __device__ __forceinline__ f32x4 tile_dot_rows(const WaveTile &w, __amdgpu_buffe
   for (int d = 0; d < 2; ++d)
 #pragma unroll
     for (int s = 0; s < 2; ++s) ax[d][s] = ldx(d, s);
-  issue_tile_loads<GPW>(w, lane, wq, sq);
+  issue_tile_loads<GPW, BOOK>(w, lane, wq, sq);
   __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before the first multiply
-  f32x4 acc = {};
+  f32x4 acc = {}, asum = {};
 #pragma unroll
   for (int jg = 0; jg < GPW; ++jg) {
     if (jg + 2 < GPW) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) ax[(jg + 2) % 3][s] = ldx(jg + 2, s);
     }
-    const half8 af[2] = {__builtin_bit_cast(half8, prep_x8(ax[jg % 3][0])),
-                         __builtin_bit_cast(half8, prep_x8(ax[jg % 3][1]))};
-    group_step<GPW, SD, 4>(acc, af, wq, sq, jg);
+    const half8 af[2] = {__builtin_bit_cast(half8, prep_act<BOOK>(ax[jg % 3][0])),
+                         __builtin_bit_cast(half8, prep_act<BOOK>(ax[jg % 3][1]))};
+    book_step<GPW, SD, 4, BOOK>(acc, asum, af, wq, sq, jg);
     // The group's epilogue happens here, not after the last group: without this the
     // compiler sinks every group's scale/bias FMAs below the last MFMA and keeps all
     // the partial products alive (register spills).
     asm volatile("" : "+v"(acc));
+  }
+  if constexpr (BOOK == kInt16) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(0.5f, asum[v], acc[v]);
   }
   return acc;
 }

@@ -113,6 +113,74 @@ def repack_blocked(w_blk: torch.Tensor, s_blk: torch.Tensor, b_blk: torch.Tensor
     return w, s, b
 
 
+BOOKS = {"int15": 1, "int16": 2, "fp4": 3}   # native codebooks (include/rlq.h RLQ_BOOK_*)
+
+
+@dataclass
+class NativeWeight:
+    """A native 4-bit matrix [N][K]: codebook codes in the packed tile layout (no
+    scale/bias section) and one fp32 scale per row. The column scale belongs to the
+    producer of the activations (it is folded into x before the product)."""
+    packed: torch.Tensor     # uint8, rlq_packed_codes_bytes(K, N)
+    s_row: torch.Tensor      # float32 [N]
+    K: int
+    N: int
+    book: str
+
+    @property
+    def code(self) -> int:
+        return BOOKS[self.book]
+
+
+def _native_rows(s_row, N, book):
+    if book not in BOOKS:
+        raise ValueError(f"unknown codebook {book!r}")
+    if s_row.dtype != torch.float32 or s_row.dim() != 1 or s_row.numel() < N or not s_row.is_contiguous():
+        raise ValueError("s_row must be a contiguous float32 vector of >= N row scales")
+
+
+def pack_native(w: torch.Tensor, s_row: torch.Tensor, book: str, stream=None) -> NativeWeight:
+    """Row-major codes (32-bit words [N][K/8], element k at bits 4*(k%8)) -> NativeWeight."""
+    if w.dtype not in (torch.int32, torch.uint32) or w.dim() != 2 or not w.is_contiguous():
+        raise TypeError("codes must be contiguous 32-bit words [N][K/8]")
+    N, K = w.shape[0], w.shape[1] * 8
+    _native_rows(s_row, N, book)
+    out = torch.empty(int(lib.load().rlq_packed_codes_bytes(K, N)), dtype=torch.uint8, device=w.device)
+    lib.call("rlq_pack_codes", _ptr(w), K, N, _ptr(out), _stream(stream))
+    return NativeWeight(out, s_row[:N], K, N, book)
+
+
+def pack_native_blocked(w_blk: torch.Tensor, s_pad: torch.Tensor, K: int, n_pad: int, row0: int, rows: int, book: str,
+                        stream=None) -> NativeWeight:
+    """Rows [row0, row0 + rows) of a blocked q4n tensor (with its padded row scales) -> NativeWeight."""
+    _native_rows(s_pad, row0 + rows, book)
+    out = torch.empty(int(lib.load().rlq_packed_codes_bytes(K, rows)), dtype=torch.uint8, device=w_blk.device)
+    lib.call("rlq_pack_native_blocked", _ptr(w_blk), K, n_pad, row0, rows, _ptr(out), _stream(stream))
+    return NativeWeight(out, s_pad[row0:row0 + rows].contiguous(), K, rows, book)
+
+
+def linear_native(x: torch.Tensor, nw: NativeWeight, out: torch.Tensor | None = None, accum: bool = False,
+                  kernel: int = KERNEL_AUTO, stream=None) -> torch.Tensor:
+    """out[m][n] (+)= s[n] * sum_k x[m][k] * L[q[n][k]] for fp16 x (column scale already applied)."""
+    if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be a row-major float16 matrix")
+    M, K, N = x.shape[0], nw.K, nw.N
+    if x.shape[1] < K:
+        raise ValueError(f"x has {x.shape[1]} columns, the weight needs {K}")
+    if out is None:
+        if accum:
+            raise ValueError("accum needs an output to add into")
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    if out.dtype != torch.float32 or out.stride(1) != 1 or out.shape[0] < M or out.shape[1] < N:
+        raise ValueError("out must be a row-major float32 [M][>=N] matrix")
+    nbytes = workspace_bytes(M, K, N)
+    ws = _WS.get(x.device, nbytes)
+    lib.call("rlq_linear_native_kernel", kernel, _ptr(x), x.stride(0), M, K, N, _ptr(nw.packed), _ptr(nw.s_row),
+             nw.code, _ptr(out), out.stride(0), 1 if accum else 0, _ptr(ws), 0 if ws is None else ws.numel(),
+             _stream(stream))
+    return out
+
+
 class _Workspaces:
     """One scratch buffer per device, grown on demand (its contents are not kept between
     calls). Calls that use it must not overlap on two streams of one device."""

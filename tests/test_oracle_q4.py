@@ -279,3 +279,13 @@ def test_reference_test_case_draws():
     assert q.max() <= 15 and sf.min() >= 0.00099 and sf.max() <= 0.012 + 2.0 ** -14   # one bf16 step
     assert np.all(np.abs(bf + 7.5 * sf) <= 0.0101 + 0.01 * np.abs(bf))
     assert x.dtype == np.float16 and np.abs(x).max() <= 2.0 and x.shape == (3, 256)
+
+
+def test_reference_native_case_draws():
+    """Native cases draw the row scales first (tests/test_linear.mm:260), then the codes."""
+    q, s, x = O.reference_native_case(2, 128, 40)
+    g = O.XorShift64()
+    first_s = [float(g.uniform(0.002, 0.02)) for _ in range(40)]
+    assert [float(v) for v in s] == first_s
+    assert [int(v) for v in q[0, :8]] == [g.next() & 15 for _ in range(8)]
+    assert x.shape == (2, 128) and s.min() >= 0.002 and s.max() < 0.02

@@ -131,6 +131,21 @@ int rlq_linear_native_kernel(int kernel, const void *x, int x_stride, int M, int
                              const float *s_row, int book, float *y, int y_stride, int accum, void *workspace,
                              size_t workspace_bytes, void *stream);
 
+/* ---------------------------------------------------------------- dense fp16 linear */
+
+/* Half-precision matrices (the MoE router, the MTP head's input projection) in MFMA
+ * operand order: rlq_packed_f16_bytes(K, N) = ceil(N/16) * (K/32) * 1024 bytes, K % 32 == 0. */
+size_t rlq_packed_f16_bytes(int K, int N);
+/* Row-major fp16 [N][K] -> packed. */
+int rlq_pack_f16(const void *w, int K, int N, void *packed, void *stream);
+/* Blocked f16b file layout ([n_pad/256][K][256] halves, tools/convert.py:218-226) rows
+ * [row0, row0+rows) -> packed. */
+int rlq_pack_f16_blocked(const void *w_blk, int K, int n_pad, int row0, int rows, void *packed, void *stream);
+/* y[m][n] (+)= sum_k x[m][k] * W[n][k], fp32 accumulation. Replaces linear_f16
+ * (kernels/linear.metal:186-225). x fp16 [M][x_stride]; y fp32 [M][y_stride]. */
+int rlq_linear_f16(const void *x, int x_stride, int M, int K, int N, const void *packed, float *y, int y_stride,
+                   int accum, void *stream);
+
 /* gsum[m][g] = sum_{k<64} x[m][64g+k], summed in order in fp32 (kernels/linear.metal:34-45). */
 int rlq_group_sums(const void *x, int x_stride, int M, int K, float *gsum, void *stream);
 

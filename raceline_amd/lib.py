@@ -44,6 +44,10 @@ SIGNATURES = {
                                   c_int, c_void_p, c_size_t, c_void_p]),
     "rlq_linear_native_kernel": (c_int, [c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int,
                                          c_void_p, c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "rlq_packed_f16_bytes": (c_size_t, [c_int, c_int]),
+    "rlq_pack_f16": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "rlq_pack_f16_blocked": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "rlq_linear_f16": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "rlq_pack_moe_gate_up": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
     "rlq_moe_max_items": (c_size_t, [c_int, c_int, c_int]),
     "rlq_moe_route": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -181,6 +181,43 @@ def linear_native(x: torch.Tensor, nw: NativeWeight, out: torch.Tensor | None = 
     return out
 
 
+@dataclass
+class DenseWeight:
+    """A half-precision matrix [N][K] in MFMA operand order (rlq_pack_f16)."""
+    packed: torch.Tensor
+    K: int
+    N: int
+
+
+def pack_f16(w: torch.Tensor, stream=None) -> DenseWeight:
+    if w.dtype != torch.float16 or w.dim() != 2 or not w.is_contiguous():
+        raise TypeError("w must be a contiguous float16 [N][K] matrix")
+    N, K = w.shape
+    out = torch.empty(int(lib.load().rlq_packed_f16_bytes(K, N)), dtype=torch.uint8, device=w.device)
+    lib.call("rlq_pack_f16", _ptr(w), K, N, _ptr(out), _stream(stream))
+    return DenseWeight(out, K, N)
+
+
+def pack_f16_blocked(w_blk: torch.Tensor, K: int, n_pad: int, row0: int, rows: int, stream=None) -> DenseWeight:
+    out = torch.empty(int(lib.load().rlq_packed_f16_bytes(K, rows)), dtype=torch.uint8, device=w_blk.device)
+    lib.call("rlq_pack_f16_blocked", _ptr(w_blk), K, n_pad, row0, rows, _ptr(out), _stream(stream))
+    return DenseWeight(out, K, rows)
+
+
+def linear_f16(x: torch.Tensor, dw: DenseWeight, out: torch.Tensor | None = None, accum: bool = False,
+               stream=None) -> torch.Tensor:
+    if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < dw.K:
+        raise ValueError("x must be a row-major float16 [M][>= K] matrix")
+    M = x.shape[0]
+    if out is None:
+        if accum:
+            raise ValueError("accum needs an output to add into")
+        out = torch.empty((M, dw.N), dtype=torch.float32, device=x.device)
+    lib.call("rlq_linear_f16", _ptr(x), x.stride(0), M, dw.K, dw.N, _ptr(dw.packed), _ptr(out), out.stride(0),
+             1 if accum else 0, _stream(stream))
+    return out
+
+
 class _Workspaces:
     """One scratch buffer per device, grown on demand (its contents are not kept between
     calls). Calls that use it must not overlap on two streams of one device."""

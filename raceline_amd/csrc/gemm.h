@@ -1,0 +1,31 @@
+// The prefill GEMM of the 4-bit formats (gemm.hip), called by the entry points of
+// linear.hip, and the small activation-sum kernels it shares with them.
+#pragma once
+
+#include "rlq_common.h"
+
+namespace rlq {
+
+struct GemmArgs {
+  const _Float16 *x;    // affine: the prepped activations [M][K]; native: x [M][x_stride]
+  const u32x4 *codes;
+  const u32x4 *sb;      // affine: scale/bias quads
+  const _Float16 *gshl; // affine: group sums as fp16 (hi, lo) pairs [M][gs_stride]
+  const float *srow;    // native books: row scales [N]
+  const float *asum;    // kInt16: activation row sums [M]
+  float *y;
+  int x_stride, M, K, N, y_stride, gs_stride;
+};
+
+// Bytes of workspace run_gemm4 needs (affine: the prepped activations and the split group
+// sums; kInt16: group and row sums; other books: none).
+size_t gemm4_workspace(int book, int M, int K);
+
+int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
+              const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st);
+
+// defined in linear.hip
+void launch_group_sums(const _Float16 *x, int x_stride, int M, int K, float *gsT, int m_pad, hipStream_t st);
+void launch_row_sums(const float *gsT, int G, int m_pad, int M, float *asum, hipStream_t st);
+
+}  // namespace rlq

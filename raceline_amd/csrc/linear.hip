@@ -11,6 +11,7 @@
 //
 // The packed layout, the MFMA operand layout and the operand trick are described in
 // q4_tile.h.
+#include "gemm.h"
 #include "q4_tile.h"
 #include "../../include/rlq.h"
 
@@ -374,134 +375,6 @@ __global__ void group_sums_kernel(const _Float16 *x, int x_stride, int M, int K,
   if (gsT) gsT[(size_t)g * m_pad + m] = sum;
 }
 
-// ================================================================== prefill GEMM (M > 8)
-//
-// Workgroup tile 128 (tokens) x 128 (features), 4 waves as 2 x 2, each 64 x 64 = 4 x 4
-// MFMA tiles of 16 x 16. Per pair of groups: the activation tile [128][128] goes through
-// LDS (shared by the two waves of a row band); each wave loads its four feature tiles'
-// packed codes (one 16-byte load per lane each) straight into B operands, turns them
-// into exact fp16 codes in registers, and two MFMA steps per group give each tile's
-// partial product; then acc += s * part + b * gsum.
-struct GemmArgs {
-  const _Float16 *x;
-  const u32x4 *codes;
-  const u32x4 *sb;      // affine: scale/bias quads
-  const float *gsT;     // affine: group sums [G][m_pad]
-  const float *srow;    // native books: row scales [N]
-  const float *asum;    // kInt16: activation row sums [m_pad]
-  float *y;
-  int x_stride, M, K, N, y_stride, m_pad;
-};
-
-constexpr int kBM = 128, kBN = 128, kLdsRow = 128 + 8;
-
-template <int SD, bool ACC, int BOOK>
-__global__ __launch_bounds__(256) void gemm_q4a_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[kBM * kLdsRow];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int c16 = lane & 15, j4 = lane >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-  const int G = a.K / kGroup, G4 = quads_of(a.K), GP = 2 * G4;
-  const int T = tiles_of(a.N);
-
-  int tile[4];
-  bool tval[4];
-#pragma unroll
-  for (int ft = 0; ft < 4; ++ft) {
-    tile[ft] = (n0 >> 4) + wn * 4 + ft;
-    tval[ft] = tile[ft] < T;
-  }
-
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{};
-
-  for (int p = 0; p < (G + 1) / 2; ++p) {
-    // activation tile [128][128] (groups 2p, 2p+1) -> LDS: 2048 chunks of 8 halves, 8 per thread
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int chunk = tid + 256 * c;
-      const int r = chunk >> 4, kc = chunk & 15;
-      const int m = m0 + r, k = 128 * p + 8 * kc;
-      half8 v = {};
-      if (m < a.M && k < a.K) v = *reinterpret_cast<const half8 *>(a.x + (size_t)m * a.x_stride + k);
-      *reinterpret_cast<half8 *>(As + r * kLdsRow + 8 * kc) = v;
-    }
-    u32x4 wq[4], sq[4];
-#pragma unroll
-    for (int ft = 0; ft < 4; ++ft) {
-      wq[ft] = tval[ft] ? a.codes[((size_t)tile[ft] * GP + p) * 64 + lane] : u32x4{};
-      if constexpr (BOOK == kAffine) sq[ft] = tval[ft] ? a.sb[((size_t)tile[ft] * G4 + (p >> 1)) * 16 + c16] : u32x4{};
-    }
-    __syncthreads();
-
-#pragma unroll
-    for (int gg = 0; gg < 2; ++gg) {
-      const int g = 2 * p + gg;
-      if (g >= G) break;
-      half8 bf[4][2];
-#pragma unroll
-      for (int ft = 0; ft < 4; ++ft)
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-          bf[ft][s] = BOOK == kAffine ? nib8_to_half8(wq[ft][2 * gg + s]) : native8_to_half8<BOOK>(wq[ft][2 * gg + s]);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        half8 af[2];
-        const _Float16 *arow = As + (wm * 64 + mt * 16 + c16) * kLdsRow + 64 * gg + 8 * j4;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(arow + 32 * s);
-        if constexpr (BOOK != kAffine) {
-          // native: one MFMA chain over all of K, the row scale at the end
-#pragma unroll
-          for (int ft = 0; ft < 4; ++ft)
-#pragma unroll
-            for (int s = 0; s < 2; ++s) acc[mt][ft] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bf[ft][s], acc[mt][ft], 0, 0, 0);
-          continue;
-        }
-        const f32x4 gq = *reinterpret_cast<const f32x4 *>(a.gsT + (size_t)g * a.m_pad + m0 + wm * 64 + mt * 16 + 4 * j4);
-#pragma unroll
-        for (int ft = 0; ft < 4; ++ft) {
-          f32x4 pp = {};
-#pragma unroll
-          for (int s = 0; s < 2; ++s) pp = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bf[ft][s], pp, 0, 0, 0);
-          const uint32_t pr = sq[ft][2 * (p & 1) + gg];
-          const float sc = scale_f32<SD>((uint16_t)(pr & 0xFFFFu));
-          const float bi = scale_f32<SD>((uint16_t)(pr >> 16));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[mt][ft][r] += sc * pp[r] + bi * gq[r];
-        }
-      }
-    }
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int ft = 0; ft < 4; ++ft) {
-      const int n = 16 * tile[ft] + c16;
-      if (n >= a.N) continue;
-      const float rs = BOOK == kAffine ? 1.0f : a.srow[n];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + mt * 16 + 4 * j4 + r;
-        if (m < a.M) {
-          float v = acc[mt][ft][r];
-          if constexpr (BOOK == kInt16) v = __builtin_fmaf(0.5f, a.asum[m], v);
-          if constexpr (BOOK != kAffine) v *= rs;
-          float *dst = a.y + (size_t)m * a.y_stride + n;
-          *dst = ACC ? *dst + v : v;
-        }
-      }
-    }
-}
-
 // asum[m] = sum over g of gsT[g][m], in order: the activation row sums the half-step
 // codebook needs.
 __global__ void row_sums_kernel(const float *gsT, int G, int m_pad, int M, float *asum) {
@@ -512,61 +385,13 @@ __global__ void row_sums_kernel(const float *gsT, int G, int m_pad, int M, float
   asum[m] = s;
 }
 
-// group sums transposed [G][m_pad], then the row sums [m_pad] (kInt16)
-static size_t gemm_workspace(int M, int K) {
-  const int m_pad = (M + kBM - 1) / kBM * kBM;
-  return (size_t)(K / kGroup + 1) * m_pad * sizeof(float);
-}
-
-template <int BOOK>
-static int launch_gemm_book(int sd, int accum, dim3 grid, hipStream_t st, const GemmArgs &a) {
-  if constexpr (BOOK == kAffine) {
-    if (sd == RLQ_BF16) {
-      if (accum) gemm_q4a_kernel<1, true, BOOK><<<grid, 256, 0, st>>>(a);
-      else gemm_q4a_kernel<1, false, BOOK><<<grid, 256, 0, st>>>(a);
-      return 0;
-    }
-  }
-  if (accum) gemm_q4a_kernel<0, true, BOOK><<<grid, 256, 0, st>>>(a);
-  else gemm_q4a_kernel<0, false, BOOK><<<grid, 256, 0, st>>>(a);
-  return 0;
-}
-
-static int run_gemm(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
-                    const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st) {
-  const int m_pad = (M + kBM - 1) / kBM * kBM;
+void launch_group_sums(const _Float16 *x, int x_stride, int M, int K, float *gsT, int m_pad, hipStream_t st) {
   const int G = K / kGroup;
-  GemmArgs a;
-  a.x = x;
-  a.codes = static_cast<const u32x4 *>(packed);
-  a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
-  a.gsT = nullptr; a.srow = srow; a.asum = nullptr; a.y = y;
-  a.x_stride = x_stride; a.M = M; a.K = K; a.N = N; a.y_stride = y_stride; a.m_pad = m_pad;
-  if (book == kAffine || book == kInt16) {
-    const size_t need = gemm_workspace(M, K);
-    RLQ_REQUIRE(ws_bytes >= need, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
-    RLQ_REQUIRE(aligned(ws, 16), "workspace must be 16-byte aligned");
-    float *gsT = static_cast<float *>(ws);
-    // rows M..m_pad of gsT only feed output rows that are never stored
-    group_sums_kernel<<<(M * G + 255) / 256, 256, 0, st>>>(x, x_stride, M, K, nullptr, gsT, m_pad);
-    RLQ_HIP(hipGetLastError());
-    a.gsT = gsT;
-    if (book == kInt16) {
-      float *asum = gsT + (size_t)G * m_pad;
-      row_sums_kernel<<<(M + 255) / 256, 256, 0, st>>>(gsT, G, m_pad, M, asum);
-      RLQ_HIP(hipGetLastError());
-      a.asum = asum;
-    }
-  }
-  const dim3 grid((N + kBN - 1) / kBN, m_pad / kBM);
-  switch (book) {
-    case kInt15: launch_gemm_book<kInt15>(sd, accum, grid, st, a); break;
-    case kInt16: launch_gemm_book<kInt16>(sd, accum, grid, st, a); break;
-    case kFp4: launch_gemm_book<kFp4>(sd, accum, grid, st, a); break;
-    default: launch_gemm_book<kAffine>(sd, accum, grid, st, a); break;
-  }
-  RLQ_HIP(hipGetLastError());
-  return 0;
+  group_sums_kernel<<<(M * G + 255) / 256, 256, 0, st>>>(x, x_stride, M, K, nullptr, gsT, m_pad);
+}
+
+void launch_row_sums(const float *gsT, int G, int m_pad, int M, float *asum, hipStream_t st) {
+  row_sums_kernel<<<(M + 255) / 256, 256, 0, st>>>(gsT, G, m_pad, M, asum);
 }
 
 static int check_linear_args(const char *fn, const void *x, int x_stride, int M, int K, int N, const void *packed,
@@ -684,8 +509,8 @@ int rlq_linear_native_kernel(int kernel, const void *x, int x_stride, int M, int
   auto st = static_cast<hipStream_t>(stream);
   auto xh = static_cast<const _Float16 *>(x);
   if (gemv) return run_gemv(book, xh, x_stride, M, K, N, packed, RLQ_F16, s_row, y, y_stride, accum, st);
-  return run_gemm(book, xh, x_stride, M, K, N, packed, RLQ_F16, s_row, y, y_stride, accum, workspace, workspace_bytes,
-                  st);
+  return run_gemm4(book, xh, x_stride, M, K, N, packed, RLQ_F16, s_row, y, y_stride, accum, workspace, workspace_bytes,
+                   st);
 }
 
 int rlq_linear_native(const void *x, int x_stride, int M, int K, int N, const void *packed, const float *s_row,
@@ -697,7 +522,9 @@ int rlq_linear_native(const void *x, int x_stride, int M, int K, int N, const vo
 
 size_t rlq_linear_workspace_bytes(int M, int K, int N) {
   if (M <= 0 || K <= 0 || N <= 0 || K % kGroup) return 0;
-  return std::max(M <= kGemvMaxM ? gemv_workspace(M, K, N) : (size_t)0, gemm_workspace(M, K));
+  // the largest of the books (the affine prefill kernel's prepped activations)
+  return std::max({M <= kGemvMaxM ? gemv_workspace(M, K, N) : (size_t)0, gemm4_workspace(kAffine, M, K),
+                   gemm4_workspace(kInt16, M, K)});
 }
 
 int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int K, int N, const void *packed,
@@ -710,8 +537,8 @@ int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int
   auto st = static_cast<hipStream_t>(stream);
   auto xh = static_cast<const _Float16 *>(x);
   if (gemv) return run_gemv(kAffine, xh, x_stride, M, K, N, packed, scale_dtype, nullptr, y, y_stride, accum, st);
-  return run_gemm(kAffine, xh, x_stride, M, K, N, packed, scale_dtype, nullptr, y, y_stride, accum, workspace,
-                  workspace_bytes, st);
+  return run_gemm4(kAffine, xh, x_stride, M, K, N, packed, scale_dtype, nullptr, y, y_stride, accum, workspace,
+                   workspace_bytes, st);
 }
 
 int rlq_linear_affine(const void *x, int x_stride, int M, int K, int N, const void *packed, int scale_dtype, float *y,

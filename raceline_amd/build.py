@@ -52,6 +52,20 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _check_defined(lib: str) -> None:
+    """Fails when the library leaves one of its own symbols undefined. A shared library
+    links with undefined symbols, and the loader only refuses it at dlopen; clang's host
+    pass can drop a kernel's launch stub without a diagnostic (a kernel template whose
+    body it skips), which shows up here as an undefined rlq:: symbol."""
+    nm = shutil.which("nm")
+    if not nm:
+        return
+    r = subprocess.run([nm, "-u", "-C", lib], capture_output=True, text=True)
+    missing = [l.strip() for l in r.stdout.splitlines() if "rlq::" in l or " rlq_" in l]
+    if missing:
+        raise RuntimeError("library leaves its own symbols undefined:\n  " + "\n  ".join(missing))
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
@@ -63,6 +77,7 @@ def build(verbose: bool = True) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"link failed:\n{r.stderr}")
+    _check_defined(tmp)
     os.replace(tmp, OUT)
     if verbose:
         print(f"built {OUT} from {len(srcs)} sources", flush=True)

@@ -3,21 +3,26 @@
 //   affine: y[m][n] = sum_g s[n][g] * (x_g . q_g)[m][n] + b[n][g] * gsum[m][g]
 //   native: y[m][n] = s[n] * (x . L(q))[m][n]  (+ 0.5 s[n] rowsum[m] for the half-step book)
 //
-// Workgroup tile 128 tokens x 256 features, 8 waves as 2 x 4, each 64 x 64 = 4 x 4
-// v_mfma_f32_16x16x32_f16 tiles. The K loop runs over group pairs (128 inputs):
+// Workgroup tile 128 tokens x 256 features, 8 waves as 2 x 4, each 64 x 64 = 2 x 2
+// v_mfma_f32_32x32x16_f16 tiles (on gfx950 this shape runs at twice the rate of
+// 16x16x32: measured 2.1 against 1.17 PFLOP/s). The K loop runs over group pairs (128 inputs):
 //  - the activation tile [128][128] of the next pair streams straight from memory into
 //    one of two LDS buffers (buffer_load ... lds: no registers, no VALU), while the MFMAs
 //    work on the other; rows are stored with their 16-byte chunks XOR-swizzled by the row
 //    so the MFMA operand reads hit 16 distinct chunks;
 //  - each wave's packed codes (one 16-byte load per lane per 16-row tile: the tile layout
 //    of q4_tile.h) and scales of the next pair are prefetched into registers;
-//  - codes become exact fp16 values in registers; a wave converts each of its 4 feature
-//    tiles once per group and reuses them over its 4 token tiles.
+//  - codes become exact fp16 values in registers; a wave converts each of its 2 feature
+//    tiles once per group and reuses them over its 2 token tiles.
 // Affine: the activations are first rewritten by a prep pass into the operand order of
-// q4_tile.h (x0, x4, x1/16, x5/16, ...), matching the cheap code conversion, and the per
-// group epilogue is a single FMA per output (acc += s * part): the bias term
-// sum_g b[n][g] gsum[m][g] is one more MFMA product at the end, over K' = 2G, with the
-// group sums split into fp16 hi + lo (exact to 2^-22) and b as the other operand.
+// q4_tile.h (x0, x4, x1/16, x5/16, ...), matching the cheap code conversion; each group's
+// scale is folded into the code operands as two exact fp16 products (s = s_hi + s_lo), so
+// the scaled products chain in the MFMA with no per-group work on the accumulators. (One
+// MFMA product per group scaled by an FMA per output instead halves the MFMA work but is
+// bound by the VALU: two FMAs per 32x32 step on top of the code conversion; it measured
+// slower.) The bias term sum_g b[n][g] gsum[m][g] is one more MFMA product at the end,
+// over K' = 2G, with the group sums split into fp16 hi + lo (exact to 2^-22) and b as the
+// other operand.
 // Native books: activations are used as they are, codes decode in element order, and the
 // products chain in the MFMA over all of K with the row scale applied at the end.
 // A row's result depends only on its own activations (MFMA rows are independent).
@@ -32,50 +37,114 @@ namespace rlq {
 constexpr int kGM = 128, kGN = 256;         // workgroup tile
 constexpr int kGThreads = 512;
 constexpr int kARowBytes = 256;             // one pair of groups: 128 fp16
-constexpr int kABufBytes = kGM * kARowBytes;
+constexpr int kABytes = kGM * kARowBytes;   // stage part: activation tile, 32 KB
+constexpr int kBBytes = (kGN / 16) * 1024;  // stage part: the 16 tiles' code kilobytes, 16 KB
+constexpr int kSBytes = (kGN / 16) * 256;   // stage part: their scale/bias quads, 4 KB
+constexpr int kStageBytes = kABytes + kBBytes + kSBytes;
+constexpr int kStages = 3;                  // loads run two group pairs ahead of the MFMAs
+
+// (1024 + a, 1024 + b) as fp16 bits -> exactly (a, b)
+__device__ __forceinline__ uint32_t sub1024_pair(uint32_t bits) {
+  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  const half2v m = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, bits) + m);
+}
+
+// (mask & a) | (~mask & b) in one v_bfi_b32. Written out because the compiler splits the
+// pattern into an and + or pair when the mask is a literal (gfx950's VOP3 encoding takes
+// no literal operand); here the mask sits in a scalar register.
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+  return r;
+}
 
 // Eight codes (oddx16 element order of q4_tile.h) -> exact normal fp16: (q0, q4),
-// (16 q1, 16 q5), (q2, q6), (16 q3, 16 q7).
-__device__ __forceinline__ half8 nib8_to_half8_oddx16_exact(uint32_t u) {
+// (16 q1, 16 q5), (q2, q6), (16 q3, 16 q7). Nine ops: each pair of codes is inserted under
+// the exponent pattern of 1024 (mg = 0x64006400, kept in a vector register) with one
+// v_bfi_b32, and 1024 is subtracted.
+__device__ __forceinline__ half8 nib8_to_half8_oddx16_exact(uint32_t u, uint32_t mg) {
   const uint32_t t = u >> 8;
   u32x4 d;
-  d[0] = magic_pair_to_f16(u & 0x000F000Fu);
-  d[1] = magic_pair_to_f16(u & 0x00F000F0u);
-  d[2] = magic_pair_to_f16(t & 0x000F000Fu);
-  d[3] = magic_pair_to_f16(t & 0x00F000F0u);
+  d[0] = sub1024_pair(bfi(0x000F000Fu, u, mg));
+  d[1] = sub1024_pair(bfi(0x00F000F0u, u, mg));
+  d[2] = sub1024_pair(bfi(0x000F000Fu, t, mg));
+  d[3] = sub1024_pair(bfi(0x00F000F0u, t, mg));
   return __builtin_bit_cast(half8, d);
 }
 
 // ------------------------------------------------------------------ affine prep pass
 
 // xp[m][k]: x in operand order (prep_x8 per 8 elements); gshl[m][2g], [2g+1]: the group
-// sum (sequential fp32, as kernels/linear.metal:42-44) split into fp16 hi and lo.
+// sum split into fp16 hi and lo. One thread per 8 activations (coalesced 16-byte loads and
+// stores); the 8 threads of a group add their partial sums with a fixed butterfly.
 __global__ void gemm_prep_kernel(const _Float16 *x, int x_stride, int M, int K, _Float16 *xp, _Float16 *gshl,
                                  int gs_stride) {
-  const int G = K / kGroup;
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= M * G) return;
-  const int m = idx / G, g = idx - m * G;
-  const u32x4 *src = reinterpret_cast<const u32x4 *>(x + (size_t)m * x_stride + (size_t)g * kGroup);
-  u32x4 *dst = reinterpret_cast<u32x4 *>(xp + (size_t)m * K + (size_t)g * kGroup);
+  const int C = K / 8;                                  // chunks per row (a multiple of 8)
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool in = idx < (long long)M * C;
+  const int m = in ? (int)(idx / C) : 0, c = in ? (int)(idx - (long long)m * C) : 0;
+  u32x4 v = {};
+  if (in) v = *reinterpret_cast<const u32x4 *>(x + (size_t)m * x_stride + 8 * c);
+  const half8 h = __builtin_bit_cast(half8, v);
   float sum = 0.0f;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const u32x4 v = src[c];
-    const half8 h = __builtin_bit_cast(half8, v);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sum += static_cast<float>(h[e]);
-    dst[c] = prep_x8(v);
+  for (int e = 0; e < 8; ++e) sum += static_cast<float>(h[e]);
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  sum += __shfl_xor(sum, 4);
+  if (!in) return;
+  *reinterpret_cast<u32x4 *>(xp + (size_t)m * K + 8 * c) = prep_x8(v);
+  if ((c & 7) == 0) {
+    const int g = c >> 3, G = C >> 3;
+    const _Float16 hi = static_cast<_Float16>(sum);
+    const _Float16 lo = static_cast<_Float16>(sum - static_cast<float>(hi));
+    gshl[(size_t)m * gs_stride + 2 * g] = hi;
+    gshl[(size_t)m * gs_stride + 2 * g + 1] = lo;
+    if (g == G - 1)   // the row's padding up to gs_stride is zero (no memset: this runs in graphs)
+      for (int k = 2 * G; k < gs_stride; ++k) gshl[(size_t)m * gs_stride + k] = (_Float16)0.0f;
   }
-  const _Float16 hi = static_cast<_Float16>(sum);
-  const _Float16 lo = static_cast<_Float16>(sum - static_cast<float>(hi));
-  gshl[(size_t)m * gs_stride + 2 * g] = hi;
-  gshl[(size_t)m * gs_stride + 2 * g + 1] = lo;
-  if (g == G - 1)   // the row's padding up to gs_stride is zero (no memset: this runs in graphs)
-    for (int k = 2 * G; k < gs_stride; ++k) gshl[(size_t)m * gs_stride + k] = (_Float16)0.0f;
 }
 
 // ------------------------------------------------------------------ the GEMM
+
+// Where one thread's 8 LDS-DMA loads of a stage come from (see gemm4_kernel).
+struct StageSrc {
+  __amdgpu_buffer_rsrc_t rx, rcode, rsb;
+  uint32_t a_off[4];
+  bool a_row[4];
+  int K, GP, G4, wave, lane;
+};
+
+__device__ __forceinline__ __attribute__((address_space(3))) void *lds_at(unsigned char *lds, int stage, int off) {
+  return (__attribute__((address_space(3))) void *)(lds + (size_t)stage * kStageBytes + off);
+}
+
+// Loads group pair p into LDS stage `stage`: 4 activation chunks (16 bytes each; inputs
+// past K and rows past M read zero), 2 code chunks of 16 bytes (tile 2 wave + i: its pair-p
+// kilobyte) and 2 scale words (quad p/2 of the same tiles).
+__device__ __forceinline__ void issue_stage(const StageSrc &s, unsigned char *lds, int p, int stage) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * (4 * s.wave + i) + (s.lane >> 4);
+    const int c = (s.lane & 15) ^ (r & 15);
+    const bool ok = s.a_row[i] && 128 * p + 8 * c < s.K;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, stage, (4 * s.wave + i) * 1024), 16,
+                                             ok ? s.a_off[i] + (uint32_t)(256 * p) : kFarOffset, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int k = 2 * s.wave + i;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rcode, lds_at(lds, stage, kABytes + k * 1024), 16,
+                                             (uint32_t)k * s.GP * 1024u + (uint32_t)p * 1024u + 16u * s.lane, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int k = 2 * s.wave + i;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rsb, lds_at(lds, stage, kABytes + kBBytes + k * 256), 4,
+                                             (uint32_t)k * s.G4 * 256u + (uint32_t)(p >> 1) * 256u + 4u * s.lane, 0, 0, 0);
+  }
+}
 
 template <int BOOK, int SD, bool ACC>
 __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
@@ -100,178 +169,194 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   const int mb = lin % mblocks, nb = lin / mblocks;
   const int m0 = mb * kGM, n0 = nb * kGN;
 
-  // activation descriptor: the whole [M][x_stride] matrix; rows >= M read zeros
+  // Every stage of the LDS ring holds, for one group pair: the activation tile (rows with
+  // their 16-byte chunks XOR-swizzled by the row), the kilobyte of codes of each of the
+  // workgroup's 16 tiles (a straight copy of the packed layout), and their scale/bias
+  // quads. Every thread issues the same 8 LDS-DMA loads per stage (4 activation chunks of
+  // 16 bytes, 2 code chunks of 16 bytes, 2 scale words), so waiting until 8 loads remain
+  // in flight waits for exactly the older stage.
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)((size_t)a.M * a.x_stride * 2));
-  // this thread's four 16-byte chunks of each activation tile
-  uint32_t a_off[4];
-  bool a_row[4];
+  const int t0 = n0 >> 4;                                 // first 16-row tile of the workgroup
+  const int tiles = max(0, min(T, t0 + 16) - t0);
+  const __amdgpu_buffer_rsrc_t rcode = make_rsrc(a.codes + (size_t)min(t0, T) * GP * 64, (uint32_t)tiles * GP * 1024u);
+  const __amdgpu_buffer_rsrc_t rsb =
+      make_rsrc(a.sb + (size_t)min(t0, T) * G4 * 16, BOOK == kAffine ? (uint32_t)tiles * G4 * 256u : 0u);
+  StageSrc src;
+  src.rx = rx; src.rcode = rcode; src.rsb = rsb;
+  src.K = a.K; src.GP = GP; src.G4 = G4; src.wave = wave; src.lane = lane;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * (4 * wave + i) + (lane >> 4);   // row within the tile
     const int c = (lane & 15) ^ (r & 15);             // logical chunk stored at this lane's slot
-    a_off[i] = (uint32_t)(((size_t)(m0 + r) * a.x_stride + 8 * c) * 2);
-    a_row[i] = m0 + r < a.M;
+    src.a_off[i] = (uint32_t)(((size_t)(m0 + r) * a.x_stride + 8 * c) * 2);
+    src.a_row[i] = m0 + r < a.M;
   }
-  auto issue_a = [&](int p, int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * (4 * wave + i) + (lane >> 4);
-      const int c = (lane & 15) ^ (r & 15);
-      const bool ok = a_row[i] && 128 * p + 8 * c < a.K;   // inputs past K read zero
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (__attribute__((address_space(3))) void *)(lds + (size_t)buf * kABufBytes + (size_t)(4 * wave + i) * 1024),
-          16, ok ? a_off[i] + (uint32_t)(256 * p) : kFarOffset, 0, 0, 0);
-    }
-  };
+  // Weights: this wave's 64 features are two 32-column MFMA tiles, each two 16-row tiles
+  // of the packed layout. The 32x32x16 MFMA only needs A and B to agree on which input k
+  // sits in which lane slot: lane l (column l%32, half h = l/32) takes, for step i of a
+  // group, the packed word 2i + h of its row, which the 16-row layout keeps in the slot of
+  // lane 16 j + c with j = (2i + h) % 4. Two 16-byte reads per lane and pair (slots h and
+  // 2 + h) bring a lane all its B operands: words h, 4 + h (first read) and 2 + h, 6 + h
+  // (second) of both groups. The A operand of step i is the natural chunk of inputs
+  // 16 i + 8 h .. +7, as the MFMA expects.
+  const int h = lane >> 5, c32 = lane & 31;
+  const int tt = c32 >> 4, cr = c32 & 15;                 // 16-row tile within the 32, row in it
 
-  // weights: this wave's 4 feature tiles
-  int tile[4];
+  f32x16 acc[2][2];
 #pragma unroll
-  for (int ft = 0; ft < 4; ++ft) tile[ft] = (n0 >> 4) + wn * 4 + ft;
-  __amdgpu_buffer_rsrc_t rw[4], rs[4];
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-  for (int ft = 0; ft < 4; ++ft) {
-    const bool tv = tile[ft] < T;
-    rw[ft] = make_rsrc(a.codes + (size_t)(tv ? tile[ft] : 0) * GP * 64, tv ? (uint32_t)GP * 1024u : 0u);
-    rs[ft] = make_rsrc(a.sb + (size_t)(tv ? tile[ft] : 0) * G4 * 16, (BOOK == kAffine && tv) ? (uint32_t)G4 * 256u : 0u);
-  }
-  u32x4 wq[4], wq_n[4];
-  uint32_t sp[4][2], sp_n[4][2];     // affine: (s|b) of groups 2p, 2p+1 per tile
-  auto issue_b = [&](int p, u32x4 (&w)[4], uint32_t (&s)[4][2]) {
-#pragma unroll
-    for (int ft = 0; ft < 4; ++ft) {
-      w[ft] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[ft], 16u * lane, (uint32_t)p * 1024u, 0));
-      if constexpr (BOOK == kAffine) {
-        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                      rs[ft], 16u * c16 + 8u * (p & 1), (uint32_t)(p >> 1) * 256u, 0));
-        s[ft][0] = v[0];
-        s[ft][1] = v[1];
-      }
-    }
-  };
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{};
-
-  issue_a(0, 0);
-  issue_b(0, wq, sp);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  issue_stage(src, lds, 0, 0);
+  if (NP > 1) issue_stage(src, lds, 1, 1);
 
   for (int p = 0; p < NP; ++p) {
-    const int buf = p & 1;
-    if (p + 1 < NP) {
-      issue_a(p + 1, buf ^ 1);
-      issue_b(p + 1, wq_n, sp_n);
-    }
-    const unsigned char *abuf = lds + (size_t)buf * kABufBytes;
+    const int stage = p % kStages;
+    // the stage of pair p is in LDS (only pair p + 1's loads may still be in flight), and
+    // every wave is past pair p - 1, whose stage the next loads overwrite
+    if (p + 1 < NP) __builtin_amdgcn_s_waitcnt(0x0F78);   // vmcnt(8): 8 loads of the next stage in flight
+    else __builtin_amdgcn_s_waitcnt(0);
+    // a bare barrier: __syncthreads() adds a workgroup fence, which waits for every LDS
+    // load in flight (the next stage's too); the explicit count above is the wait. The
+    // memory clobber keeps the compiler from moving LDS reads across it.
+    asm volatile("s_barrier" ::: "memory");
+    if (p + 2 < NP) issue_stage(src, lds, p + 2, (p + 2) % kStages);
+    const unsigned char *sbase = lds + (size_t)stage * kStageBytes;
+    const unsigned char *abuf = sbase, *bbuf = sbase + kABytes, *sbuf = sbase + kABytes + kBBytes;
+    u32x4 wq[2][2];
+    uint32_t sp[2][2];
 #pragma unroll
-    for (int gg = 0; gg < 2; ++gg) {
-      half8 bf[4][2];
+    for (int nt = 0; nt < 2; ++nt) {
+      const int k = wn * 4 + nt * 2 + tt;                 // the lane's 16-row tile in the workgroup
 #pragma unroll
-      for (int ft = 0; ft < 4; ++ft)
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const uint32_t u = wq[ft][2 * gg + s];
-          if constexpr (BOOK == kAffine) bf[ft][s] = nib8_to_half8_oddx16_exact(u);
-          else bf[ft][s] = native8_to_half8<BOOK>(u);
-        }
-      float sc[4];
+      for (int ld = 0; ld < 2; ++ld)
+        wq[nt][ld] = *reinterpret_cast<const u32x4 *>(bbuf + k * 1024 + 256 * (h + 2 * ld) + 16 * cr);
       if constexpr (BOOK == kAffine) {
 #pragma unroll
-        for (int ft = 0; ft < 4; ++ft) sc[ft] = scale_f32<SD>((uint16_t)(sp[ft][gg] & 0xFFFFu));
-      }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const int r = wm * 64 + mt * 16 + c16;
-        half8 af[2];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int c = 8 * gg + 4 * s + j4;
-          af[s] = *reinterpret_cast<const half8 *>(abuf + r * kARowBytes + ((c ^ c16) << 4));
-        }
-#pragma unroll
-        for (int ft = 0; ft < 4; ++ft) {
-          if constexpr (BOOK == kAffine) {
-            f32x4 pp = {};
-#pragma unroll
-            for (int s = 0; s < 2; ++s) pp = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bf[ft][s], pp, 0, 0, 0);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc[mt][ft][v] = __builtin_fmaf(sc[ft], pp[v], acc[mt][ft][v]);
-          } else {
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-              acc[mt][ft] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bf[ft][s], acc[mt][ft], 0, 0, 0);
-          }
-        }
+        for (int gg = 0; gg < 2; ++gg)
+          sp[nt][gg] = *reinterpret_cast<const uint32_t *>(sbuf + k * 256 + 16 * cr + 4 * (2 * (p & 1) + gg));
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);     // the next pair's activations (LDS) and weights (registers)
-    __syncthreads();                   // ... are there for every wave, and this buffer is free
 #pragma unroll
-    for (int ft = 0; ft < 4; ++ft) {
-      wq[ft] = wq_n[ft];
-      sp[ft][0] = sp_n[ft][0];
-      sp[ft][1] = sp_n[ft][1];
+    for (int gg = 0; gg < 2; ++gg) {
+      half8 bf[2][4];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // step i uses word 2i + h: read (i & 1), element 2 gg + (i >> 1)
+          const uint32_t u = wq[nt][i & 1][2 * gg + (i >> 1)];
+          if constexpr (BOOK == kAffine) bf[nt][i] = nib8_to_half8_oddx16_exact(u, a.magic);
+          else bf[nt][i] = native8_to_half8<BOOK>(u);
+        }
+      half8 af[2][4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int r = wm * 64 + mt * 32 + c32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = 8 * gg + 2 * i + h;
+          af[mt][i] = *reinterpret_cast<const half8 *>(abuf + r * kARowBytes + ((c ^ (r & 15)) << 4));
+        }
+      }
+      if constexpr (BOOK == kAffine) {
+        // acc += s * (x_g . q_g): one FMA per output per group. Four independent
+        // accumulators between an MFMA and the next one that reads its result.
+        f32x16 pp[2][2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) pp[mt][nt] = f32x16{};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+              pp[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt][i], bf[nt][i], pp[mt][nt], 0, 0, 0);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const float sc = scale_f32<SD>((uint16_t)(sp[nt][gg] & 0xFFFFu));
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[mt][nt][v] = __builtin_fmaf(sc, pp[mt][nt][v], acc[mt][nt][v]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+              acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt][i], bf[nt][i], acc[mt][nt], 0, 0, 0);
+      }
     }
+  }
+
+  // the bias term and the row scales read the weights' scale quads straight from memory
+  __amdgpu_buffer_rsrc_t rs[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int tn = t0 + wn * 4 + nt * 2;
+    const int tv = max(0, min(T, tn + 2) - tn);
+    rs[nt] = make_rsrc(a.sb + (size_t)min(tn, T) * G4 * 16, BOOK == kAffine ? (uint32_t)tv * G4 * 256u : 0u);
   }
 
   if constexpr (BOOK == kAffine) {
-    // acc += sum_g b[n][g] * gsum[m][g]: an MFMA product over K' = 2G (hi, lo per group)
+    // acc += sum_g b[n][g] * gsum[m][g]: an MFMA product over K' = 2G, the group sums as
+    // (hi, lo) pairs. Step st covers k' = 16 st .. +15; lane half h holds k' 16 st + 8 h
+    // .. +7, i.e. the (hi, lo) of groups 8 st + 4 h .. +3: b of those groups, each twice.
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.gshl, (uint32_t)((size_t)a.M * a.gs_stride * 2));
-    const int steps = a.gs_stride / 32;
+    const int steps = a.gs_stride / 16;
     for (int st = 0; st < steps; ++st) {
-      half8 bb[4];
+      const int q = 2 * st + h;                      // quad of groups 4q .. 4q+3
+      half8 bb[2];
 #pragma unroll
-      for (int ft = 0; ft < 4; ++ft) {
-        const int q = 4 * st + j4;                   // quad of groups 4q .. 4q+3
+      for (int nt = 0; nt < 2; ++nt) {
         const u32x4 v = q < G4 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                               rs[ft], 16u * c16, (uint32_t)q * 256u, 0))
+                                                               rs[nt], (uint32_t)tt * G4 * 256u + 16u * cr, (uint32_t)q * 256u, 0))
                                : u32x4{};
         u32x4 d;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint32_t bbits = v[e] >> 16;
-          uint32_t h;
+          uint32_t hb;
           if constexpr (SD == 0) {
-            h = bbits;
+            hb = bbits;
           } else {
-            h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__uint_as_float(bbits << 16)));
+            hb = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__uint_as_float(bbits << 16)));
           }
-          d[e] = h | (h << 16);                       // (b, b): times gsum hi and lo
+          d[e] = hb | (hb << 16);                     // (b, b): times gsum hi and lo
         }
-        bb[ft] = __builtin_bit_cast(half8, d);
+        bb[nt] = __builtin_bit_cast(half8, d);
       }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const int m = m0 + wm * 64 + mt * 16 + c16;
+      for (int mt = 0; mt < 2; ++mt) {
+        const int m = m0 + wm * 64 + mt * 32 + c32;
         const half8 ag = __builtin_bit_cast(
             half8, __builtin_amdgcn_raw_buffer_load_b128(
-                       rg, m < a.M ? (uint32_t)(((size_t)m * a.gs_stride + 32 * st + 8 * j4) * 2) : kFarOffset, 0, 0));
-        // the bias MFMA uses K' = 32 per step: lane (c16, j4) holds k' = 8 j4 .. +7, i.e.
-        // groups 4 j4' .. +3 of this step (two k' per group)
+                       rg, m < a.M ? (uint32_t)(((size_t)m * a.gs_stride + 16 * st + 8 * h) * 2) : kFarOffset, 0, 0));
 #pragma unroll
-        for (int ft = 0; ft < 4; ++ft) acc[mt][ft] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ag, bb[ft], acc[mt][ft], 0, 0, 0);
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ag, bb[nt], acc[mt][nt], 0, 0, 0);
       }
     }
   }
 
+  // D of a 32x32 tile: lane l holds column l%32, rows 8 (v/4) + 4 (l/32) + v%4
 #pragma unroll
-  for (int ft = 0; ft < 4; ++ft) {
-    const int n = 16 * tile[ft] + c16;
+  for (int nt = 0; nt < 2; ++nt) {
+    const int n = n0 + wn * 64 + nt * 32 + c32;
     if (n >= a.N) continue;
     const float rs_n = BOOK == kAffine ? 1.0f : a.srow[n];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = m0 + wm * 64 + mt * 16 + 4 * j4 + v;
+      for (int v = 0; v < 16; ++v) {
+        const int m = m0 + wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
         if (m < a.M) {
-          float val = acc[mt][ft][v];
+          float val = acc[mt][nt][v];
           if constexpr (BOOK == kInt16) val = __builtin_fmaf(0.5f, a.asum[m], val);
           if constexpr (BOOK != kAffine) val *= rs_n;
           float *dst = a.y + (size_t)m * a.y_stride + n;
@@ -314,6 +399,7 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
   RLQ_REQUIRE(need == 0 || aligned(ws, 256), "workspace must be 256-byte aligned");
   RLQ_REQUIRE((size_t)M * std::max(x_stride, K) * 2 < (1ull << 31), "prefill kernel: x spans more than 2 GiB");
   GemmArgs a = {};
+  a.magic = 0x64006400u;
   a.codes = static_cast<const u32x4 *>(packed);
   a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
   a.srow = srow;
@@ -323,7 +409,8 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
     const int gs_stride = (2 * G + 31) / 32 * 32;
     _Float16 *xp = static_cast<_Float16 *>(ws);
     _Float16 *gshl = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + ((size_t)M * K * 2 + 255) / 256 * 256);
-    gemm_prep_kernel<<<(M * G + 255) / 256, 256, 0, st>>>(x, x_stride, M, K, xp, gshl, gs_stride);
+    const long long chunks = (long long)M * (K / 8);
+    gemm_prep_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, st>>>(x, x_stride, M, K, xp, gshl, gs_stride);
     RLQ_HIP(hipGetLastError());
     a.x = xp; a.x_stride = K; a.gshl = gshl; a.gs_stride = gs_stride;
   } else {
@@ -339,7 +426,7 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
   }
   const int mblocks = (M + kGM - 1) / kGM, nblocks = (N + kGN - 1) / kGN;
   const dim3 grid(mblocks * nblocks);
-  const size_t lds = 2 * (size_t)kABufBytes;
+  const size_t lds = (size_t)kStages * kStageBytes;
   switch (book) {
     case kInt15: launch_gemm4_inst<kInt15, 0>(accum, grid, lds, st, a); break;
     case kInt16: launch_gemm4_inst<kInt16, 0>(accum, grid, lds, st, a); break;

@@ -3,26 +3,23 @@
 //   affine: y[m][n] = sum_g s[n][g] * (x_g . q_g)[m][n] + b[n][g] * gsum[m][g]
 //   native: y[m][n] = s[n] * (x . L(q))[m][n]  (+ 0.5 s[n] rowsum[m] for the half-step book)
 //
-// Workgroup tile 128 tokens x 256 features, 8 waves as 2 x 4, each 64 x 64 = 2 x 2
-// v_mfma_f32_32x32x16_f16 tiles (on gfx950 this shape runs at twice the rate of
-// 16x16x32: measured 2.1 against 1.17 PFLOP/s). The K loop runs over group pairs (128 inputs):
-//  - the activation tile [128][128] of the next pair streams straight from memory into
-//    one of two LDS buffers (buffer_load ... lds: no registers, no VALU), while the MFMAs
-//    work on the other; rows are stored with their 16-byte chunks XOR-swizzled by the row
-//    so the MFMA operand reads hit 16 distinct chunks;
-//  - each wave's packed codes (one 16-byte load per lane per 16-row tile: the tile layout
-//    of q4_tile.h) and scales of the next pair are prefetched into registers;
-//  - codes become exact fp16 values in registers; a wave converts each of its 2 feature
-//    tiles once per group and reuses them over its 2 token tiles.
+// Workgroup tile 128 tokens x 256 features, 8 waves; each wave owns 32 features over all
+// 128 tokens (four v_mfma_f32_32x32x16_f16 tiles; on gfx950 this shape runs at twice the
+// rate of 16x16x32), so each code is converted to fp16 once per workgroup.
+//  - A 3-stage LDS ring holds, per group pair (128 inputs), the activation tile, the
+//    workgroup's packed codes and its scale/bias quads, all filled by LDS-DMA
+//    (buffer_load ... lds: no registers, no VALU) two pairs ahead of use. Activation rows
+//    are stored with their 16-byte chunks XOR-swizzled by the row, so the MFMA operand
+//    reads hit distinct banks.
+//  - Codes become exact fp16 values in registers (bit-field insert under the exponent of
+//    1024, minus 1024).
+//  - The 32 MFMAs of a pair run in a fixed order with each A fragment read from LDS 8
+//    MFMAs ahead; affine group products are scaled into the fp32 accumulators by FMAs
+//    interleaved with the MFMAs of the next half-group.
 // Affine: the activations are first rewritten by a prep pass into the operand order of
-// q4_tile.h (x0, x4, x1/16, x5/16, ...), matching the cheap code conversion; each group's
-// scale is folded into the code operands as two exact fp16 products (s = s_hi + s_lo), so
-// the scaled products chain in the MFMA with no per-group work on the accumulators. (One
-// MFMA product per group scaled by an FMA per output instead halves the MFMA work but is
-// bound by the VALU: two FMAs per 32x32 step on top of the code conversion; it measured
-// slower.) The bias term sum_g b[n][g] gsum[m][g] is one more MFMA product at the end,
-// over K' = 2G, with the group sums split into fp16 hi + lo (exact to 2^-22) and b as the
-// other operand.
+// q4_tile.h (x0, x4, x1/16, x5/16, ...), matching the cheap code conversion. The bias term
+// sum_g b[n][g] gsum[m][g] is one more MFMA product at the end, over K' = 2G, with the
+// group sums split into fp16 hi + lo (exact to 2^-22) and b as the other operand.
 // Native books: activations are used as they are, codes decode in element order, and the
 // products chain in the MFMA over all of K with the row scale applied at the end.
 // A row's result depends only on its own activations (MFMA rows are independent).
@@ -146,14 +143,36 @@ __device__ __forceinline__ void issue_stage(const StageSrc &s, unsigned char *ld
   }
 }
 
+
+// The B reads of a pair (two 16-byte code slots) and, affine, its two scale words.
+template <int BOOK>
+__device__ __forceinline__ void read_pair_head(const unsigned char *lds, uint32_t boff, uint32_t soff, int p,
+                                               u32x4 (&wq)[2], uint32_t (&sp)[2]) {
+  const unsigned char *base = lds + (size_t)(p % kStages) * kStageBytes;
+  wq[0] = *reinterpret_cast<const u32x4 *>(base + boff);
+  wq[1] = *reinterpret_cast<const u32x4 *>(base + boff + 512);
+  if constexpr (BOOK == kAffine) {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = *reinterpret_cast<const u32x2 *>(base + soff + 8 * (p & 1));
+    sp[0] = v[0];
+    sp[1] = v[1];
+  }
+}
+
+
+// A fragment of step j of a pair (see gemm4_kernel): token tile 2 ((j >> 3) & 1) + (j & 1),
+// 32 rows of 256 bytes apart per tile, chunk of step (j >> 1) & 3 of group j >> 4.
+__device__ __forceinline__ half8 read_frag(const unsigned char *lds, int stage, const uint32_t (&aoff)[2][4], int j) {
+  const int gg = j >> 4, mt = 2 * ((j >> 3) & 1) + (j & 1), i = (j >> 1) & 3;
+  return *reinterpret_cast<const half8 *>(lds + (size_t)stage * kStageBytes + mt * 32 * kARowBytes + aoff[gg][i]);
+}
+
 template <int BOOK, int SD, bool ACC>
 __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c16 = lane & 15, j4 = lane >> 4;
-  const int wm = wave >> 2, wn = wave & 3;
   const int G = a.K / kGroup, G4 = quads_of(a.K), GP = 2 * G4;
   const int NP = (G + 1) / 2;                        // group pairs with real groups
   const int T = tiles_of(a.N);
@@ -191,177 +210,175 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
     src.a_off[i] = (uint32_t)(((size_t)(m0 + r) * a.x_stride + 8 * c) * 2);
     src.a_row[i] = m0 + r < a.M;
   }
-  // Weights: this wave's 64 features are two 32-column MFMA tiles, each two 16-row tiles
-  // of the packed layout. The 32x32x16 MFMA only needs A and B to agree on which input k
-  // sits in which lane slot: lane l (column l%32, half h = l/32) takes, for step i of a
-  // group, the packed word 2i + h of its row, which the 16-row layout keeps in the slot of
-  // lane 16 j + c with j = (2i + h) % 4. Two 16-byte reads per lane and pair (slots h and
-  // 2 + h) bring a lane all its B operands: words h, 4 + h (first read) and 2 + h, 6 + h
-  // (second) of both groups. The A operand of step i is the natural chunk of inputs
-  // 16 i + 8 h .. +7, as the MFMA expects.
+
+  // Each wave owns 32 features (one 32-column MFMA tile = the workgroup's 16-row tiles
+  // 2 wave and 2 wave + 1) over all 128 tokens (four 32-row MFMA tiles), so every code is
+  // converted once per workgroup. The 32x32x16 MFMA only needs A and B to agree on which
+  // input k sits in which lane slot: lane l (column l%32, half h = l/32) takes, for step i
+  // of a group, the packed word 2i + h of its row, which the 16-row layout keeps in the
+  // slot of lane 16 j + c with j = (2i + h) % 4. Two 16-byte reads per lane and pair
+  // (slots h and 2 + h) bring a lane all its B operands: words h, 4 + h (first read) and
+  // 2 + h, 6 + h (second) of both groups. The A operand of step i is the natural chunk of
+  // inputs 16 i + 8 h .. +7, as the MFMA expects.
   const int h = lane >> 5, c32 = lane & 31;
   const int tt = c32 >> 4, cr = c32 & 15;                 // 16-row tile within the 32, row in it
-
-  f32x16 acc[2][2];
+  const int kt = 2 * wave + tt;                           // the lane's 16-row tile in the workgroup
+  uint32_t aoff[2][4];                                    // A fragment offsets within a stage
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int gg = 0; gg < 2; ++gg)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int i = 0; i < 4; ++i) aoff[gg][i] = (uint32_t)(c32 * kARowBytes + (((8 * gg + 2 * i + h) ^ cr) << 4));
+  const uint32_t boff = (uint32_t)(kABytes + kt * 1024 + 256 * h + 16 * cr);
+  const uint32_t soff = (uint32_t)(kABytes + kBBytes + kt * 256 + 16 * cr);
 
+  // The K loop is software-pipelined over the 32 MFMAs of a group pair, in a fixed order:
+  // step j = 16 gg + 8 half + 2 i + t multiplies token tile mt = 2 half + t by the codes of
+  // step i of group gg. Every A fragment feeds exactly one MFMA, and is read from LDS 8
+  // steps before it (a sliding window of 8 fragments in registers). Affine: each group
+  // product is scaled into the accumulators by FMAs that run beside the next half's
+  // MFMAs (tiles 0, 1 of a group during its steps 8..15, tiles 2, 3 during the next
+  // group's steps 0..7), four FMAs per MFMA, so no instruction waits on a result issued
+  // just before it. The barrier that hands stage p + 1 over sits before step 24 of pair
+  // p: by then every wave has issued all its reads of stage p, and the first 8 fragments
+  // of pair p + 1 are read during steps 24..31.
+  f32x16 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = f32x16{};
+  f32x16 pp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pp[i] = f32x16{};
+  float sc_prev = 0.0f;
+  half8 carry[8];                                         // fragments 0..7 of the next pair
+  u32x4 wq[2];
+  uint32_t sp[2] = {0u, 0u};
+
+  // Every stage issue loads a real pair: past the last pair the index is clamped (a
+  // duplicate of the last pair into a stage nobody reads any more), so exactly two
+  // stages are always in flight and one wait count fits every hand-over.
   issue_stage(src, lds, 0, 0);
-  if (NP > 1) issue_stage(src, lds, 1, 1);
+  issue_stage(src, lds, min(1, NP - 1), 1);
+  __builtin_amdgcn_s_waitcnt(0x0F78);                     // vmcnt(8): stage 0 in place, 1 may fly
+  asm volatile("s_barrier" ::: "memory");
+  issue_stage(src, lds, min(2, NP - 1), 2);
+  read_pair_head<BOOK>(lds, boff, soff, 0, wq, sp);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) carry[j] = read_frag(lds, 0, aoff, j);
 
   for (int p = 0; p < NP; ++p) {
     const int stage = p % kStages;
-    // the stage of pair p is in LDS (only pair p + 1's loads may still be in flight), and
-    // every wave is past pair p - 1, whose stage the next loads overwrite
-    if (p + 1 < NP) __builtin_amdgcn_s_waitcnt(0x0F78);   // vmcnt(8): 8 loads of the next stage in flight
-    else __builtin_amdgcn_s_waitcnt(0);
-    // a bare barrier: __syncthreads() adds a workgroup fence, which waits for every LDS
-    // load in flight (the next stage's too); the explicit count above is the wait. The
-    // memory clobber keeps the compiler from moving LDS reads across it.
-    asm volatile("s_barrier" ::: "memory");
-    if (p + 2 < NP) issue_stage(src, lds, p + 2, (p + 2) % kStages);
-    const unsigned char *sbase = lds + (size_t)stage * kStageBytes;
-    const unsigned char *abuf = sbase, *bbuf = sbase + kABytes, *sbuf = sbase + kABytes + kBBytes;
-    u32x4 wq[2][2];
-    uint32_t sp[2][2];
+    const bool more = p + 1 < NP;
+    half8 fr[32];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int k = wn * 4 + nt * 2 + tt;                 // the lane's 16-row tile in the workgroup
+    for (int j = 0; j < 8; ++j) fr[j] = carry[j];
+    half8 bf[4];
+    float sc = 0.0f;
 #pragma unroll
-      for (int ld = 0; ld < 2; ++ld)
-        wq[nt][ld] = *reinterpret_cast<const u32x4 *>(bbuf + k * 1024 + 256 * (h + 2 * ld) + 16 * cr);
-      if constexpr (BOOK == kAffine) {
-#pragma unroll
-        for (int gg = 0; gg < 2; ++gg)
-          sp[nt][gg] = *reinterpret_cast<const uint32_t *>(sbuf + k * 256 + 16 * cr + 4 * (2 * (p & 1) + gg));
+    for (int j = 0; j < 32; ++j) {
+      const int gg = j >> 4, half = (j >> 3) & 1, i = (j >> 1) & 3, t = j & 1, mt = 2 * half + t;
+      if (j == 24 && more) {
+        // hand over stage p + 1: this wave's reads of stage p are issued and complete,
+        // and stage p + 1 has landed for every wave
+        __builtin_amdgcn_s_waitcnt(0x0078);                   // lgkmcnt(0) vmcnt(8): stage p + 2 may fly
+        asm volatile("s_barrier" ::: "memory");
+        issue_stage(src, lds, min(p + 3, NP - 1), (p + 3) % kStages);
+        read_pair_head<BOOK>(lds, boff, soff, p + 1, wq, sp);   // the last codes of pair p were read at step 22
       }
-    }
-#pragma unroll
-    for (int gg = 0; gg < 2; ++gg) {
-      half8 bf[2][4];
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // step i uses word 2i + h: read (i & 1), element 2 gg + (i >> 1)
-          const uint32_t u = wq[nt][i & 1][2 * gg + (i >> 1)];
-          if constexpr (BOOK == kAffine) bf[nt][i] = nib8_to_half8_oddx16_exact(u, a.magic);
-          else bf[nt][i] = native8_to_half8<BOOK>(u);
-        }
-      half8 af[2][4];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int r = wm * 64 + mt * 32 + c32;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int c = 8 * gg + 2 * i + h;
-          af[mt][i] = *reinterpret_cast<const half8 *>(abuf + r * kARowBytes + ((c ^ (r & 15)) << 4));
-        }
+      // (past the last pair the carried reads see a stale stage, and are not used)
+      if (j + 8 < 32) fr[j + 8] = read_frag(lds, stage, aoff, j + 8);
+      else carry[j - 24] = read_frag(lds, (p + 1) % kStages, aoff, j - 24);
+      if ((j & 15) == 0 && BOOK == kAffine) sc = scale_f32<SD>((uint16_t)(sp[gg] & 0xFFFFu));
+      if ((j & 15) < 8 && t == 0) {
+        // codes of step i, group gg: word 2i + h, i.e. read (i & 1), element 2 gg + (i >> 1)
+        const uint32_t u = wq[i & 1][2 * gg + (i >> 1)];
+        if constexpr (BOOK == kAffine) bf[i] = nib8_to_half8_oddx16_exact(u, a.magic);
+        else bf[i] = native8_to_half8<BOOK>(u);
       }
       if constexpr (BOOK == kAffine) {
-        // acc += s * (x_g . q_g): one FMA per output per group. Four independent
-        // accumulators between an MFMA and the next one that reads its result.
-        f32x16 pp[2][2];
+        pp[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[j], bf[i], i == 0 ? f32x16{} : pp[mt], 0, 0, 0);
+        // four FMAs of the other half: tiles 2, 3 (previous group, scale sc_prev) during
+        // steps 0..7 of a group, tiles 0, 1 (this group, scale sc) during steps 8..15
+        const int k = j & 7;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) pp[mt][nt] = f32x16{};
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-              pp[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt][i], bf[nt][i], pp[mt][nt], 0, 0, 0);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const float sc = scale_f32<SD>((uint16_t)(sp[nt][gg] & 0xFFFFu));
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[mt][nt][v] = __builtin_fmaf(sc, pp[mt][nt][v], acc[mt][nt][v]);
+        for (int e = 0; e < 4; ++e) {
+          const int idx = 4 * k + e, ft = idx >> 4, v = idx & 15;
+          if (half == 0) acc[2 + ft][v] = __builtin_fmaf(sc_prev, pp[2 + ft][v], acc[2 + ft][v]);
+          else acc[ft][v] = __builtin_fmaf(sc, pp[ft][v], acc[ft][v]);
         }
+        // keep the four FMAs in this step: the compiler otherwise sinks them into clumps
+        // after the MFMAs, which keeps more group products alive than registers allow
+        const int ft = (4 * k) >> 4;
+        if (half == 0) asm volatile("" : "+v"(acc[2 + ft]));
+        else asm volatile("" : "+v"(acc[ft]));
+        if ((j & 15) == 15) sc_prev = sc;
       } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-              acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt][i], bf[nt][i], acc[mt][nt], 0, 0, 0);
+        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[j], bf[i], acc[mt], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-
-  // the bias term and the row scales read the weights' scale quads straight from memory
-  __amdgpu_buffer_rsrc_t rs[2];
+  __builtin_amdgcn_s_waitcnt(0);                          // the clamped duplicates have landed
+  if constexpr (BOOK == kAffine) {
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int tn = t0 + wn * 4 + nt * 2;
-    const int tv = max(0, min(T, tn + 2) - tn);
-    rs[nt] = make_rsrc(a.sb + (size_t)min(tn, T) * G4 * 16, BOOK == kAffine ? (uint32_t)tv * G4 * 256u : 0u);
+    for (int v = 0; v < 16; ++v) {
+      acc[2][v] = __builtin_fmaf(sc_prev, pp[2][v], acc[2][v]);
+      acc[3][v] = __builtin_fmaf(sc_prev, pp[3][v], acc[3][v]);
+    }
   }
 
   if constexpr (BOOK == kAffine) {
     // acc += sum_g b[n][g] * gsum[m][g]: an MFMA product over K' = 2G, the group sums as
     // (hi, lo) pairs. Step st covers k' = 16 st .. +15; lane half h holds k' 16 st + 8 h
     // .. +7, i.e. the (hi, lo) of groups 8 st + 4 h .. +3: b of those groups, each twice.
+    // The scale quads come straight from memory.
+    const int tn = t0 + 2 * wave;
+    const int tv = max(0, min(T, tn + 2) - tn);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sb + (size_t)min(tn, T) * G4 * 16, (uint32_t)tv * G4 * 256u);
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.gshl, (uint32_t)((size_t)a.M * a.gs_stride * 2));
     const int steps = a.gs_stride / 16;
     for (int st = 0; st < steps; ++st) {
       const int q = 2 * st + h;                      // quad of groups 4q .. 4q+3
-      half8 bb[2];
+      const u32x4 v = q < G4 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             rs, (uint32_t)tt * G4 * 256u + 16u * cr, (uint32_t)q * 256u, 0))
+                             : u32x4{};
+      u32x4 d;
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const u32x4 v = q < G4 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                               rs[nt], (uint32_t)tt * G4 * 256u + 16u * cr, (uint32_t)q * 256u, 0))
-                               : u32x4{};
-        u32x4 d;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t bbits = v[e] >> 16;
-          uint32_t hb;
-          if constexpr (SD == 0) {
-            hb = bbits;
-          } else {
-            hb = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__uint_as_float(bbits << 16)));
-          }
-          d[e] = hb | (hb << 16);                     // (b, b): times gsum hi and lo
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t bbits = v[e] >> 16;
+        uint32_t hb;
+        if constexpr (SD == 0) {
+          hb = bbits;
+        } else {
+          hb = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__uint_as_float(bbits << 16)));
         }
-        bb[nt] = __builtin_bit_cast(half8, d);
+        d[e] = hb | (hb << 16);                       // (b, b): times gsum hi and lo
       }
+      const half8 bb = __builtin_bit_cast(half8, d);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int m = m0 + wm * 64 + mt * 32 + c32;
+      for (int mt = 0; mt < 4; ++mt) {
+        const int m = m0 + mt * 32 + c32;
         const half8 ag = __builtin_bit_cast(
             half8, __builtin_amdgcn_raw_buffer_load_b128(
                        rg, m < a.M ? (uint32_t)(((size_t)m * a.gs_stride + 16 * st + 8 * h) * 2) : kFarOffset, 0, 0));
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ag, bb[nt], acc[mt][nt], 0, 0, 0);
+        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ag, bb, acc[mt], 0, 0, 0);
       }
     }
   }
 
   // D of a 32x32 tile: lane l holds column l%32, rows 8 (v/4) + 4 (l/32) + v%4
+  const int n = n0 + 32 * wave + c32;
+  if (n >= a.N) return;
+  const float rs_n = BOOK == kAffine ? 1.0f : a.srow[n];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int n = n0 + wn * 64 + nt * 32 + c32;
-    if (n >= a.N) continue;
-    const float rs_n = BOOK == kAffine ? 1.0f : a.srow[n];
+  for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (m < a.M) {
-          float val = acc[mt][nt][v];
-          if constexpr (BOOK == kInt16) val = __builtin_fmaf(0.5f, a.asum[m], val);
-          if constexpr (BOOK != kAffine) val *= rs_n;
-          float *dst = a.y + (size_t)m * a.y_stride + n;
-          *dst = ACC ? *dst + val : val;
-        }
+    for (int v = 0; v < 16; ++v) {
+      const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (m < a.M) {
+        float val = acc[mt][v];
+        if constexpr (BOOK == kInt16) val = __builtin_fmaf(0.5f, a.asum[m], val);
+        if constexpr (BOOK != kAffine) val *= rs_n;
+        float *dst = a.y + (size_t)m * a.y_stride + n;
+        *dst = ACC ? *dst + val : val;
       }
     }
   }

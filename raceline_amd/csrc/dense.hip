@@ -78,7 +78,8 @@ __global__ __launch_bounds__(1024) void dense_f16_kernel(DenseArgs a) {
       const int st = b0 + i;   // relative to s0; out-of-range loads return zeros
       xb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                            rx, live && s0 + st < s1 ? xoff + (uint32_t)st * 64u : kFarOffset, 0, 0));
-      wb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, 16u * lane, (uint32_t)st * 1024u,
+      // the whole offset in the range-checked vector operand: steps past the wave's range read zeros
+      wb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, 16u * lane + (uint32_t)st * 1024u, 0,
                                                                              kNonTemporal));
     }
 #pragma unroll

@@ -117,17 +117,21 @@ __device__ __forceinline__ WaveTile wave_tile(const u32x4 *codes, const u32x4 *s
 }
 
 // Every code load of the wave's part and (affine) every scale/bias load, issued at once
-// (non-temporal).
+// (non-temporal). The whole offset goes in the vector offset operand: only that part
+// (with the instruction's immediate) is range-checked against the descriptor; the scalar
+// offset operand is not, so loads past the wave's part would read whatever follows.
 template <int GPW, int BOOK = kAffine>
 __device__ __forceinline__ void issue_tile_loads(const WaveTile &w, int lane, u32x4 (&wq)[GPW / 2],
                                                  u32x4 (&sq)[GPW / 4]) {
 #pragma unroll
   for (int pp = 0; pp < GPW / 2; ++pp)
-    wq[pp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w.rw, 16u * lane, (uint32_t)pp * 1024u, kNonTemporal));
+    wq[pp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w.rw, 16u * lane + (uint32_t)pp * 1024u, 0,
+                                                                             kNonTemporal));
   if constexpr (BOOK == kAffine) {
 #pragma unroll
     for (int qq = 0; qq < GPW / 4; ++qq)
-      sq[qq] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w.rs, 16u * (lane & 15), (uint32_t)qq * 256u, kNonTemporal));
+      sq[qq] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             w.rs, 16u * (lane & 15) + (uint32_t)qq * 256u, 0, kNonTemporal));
   }
 }
 

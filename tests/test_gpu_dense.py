@@ -61,3 +61,26 @@ def test_dense_blocked_parts(gpu):
         torch.cuda.synchronize()
         ref = x.astype(np.float64) @ W[row0:row0 + rows].astype(np.float64).T
         O.check_close(y.cpu().numpy(), ref, TOL, f"f16 blocked part {row0}")
+
+
+def test_dense_reads_nothing_past_the_weight(gpu):
+    """K = 10240 splits into 16 waves of 24 steps of which the last wave has only 20:
+    its 4 steps past the range must read zeros, not the all-ones bytes (NaN as fp16) that
+    follow the packed matrix in its buffer."""
+    import torch
+
+    from raceline_amd import ops
+
+    rng = np.random.default_rng(12)
+    M, K, N = 2, 10240, 40
+    W = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    dw = ops.pack_f16(to_dev(W, gpu))
+    nbytes = dw.packed.numel()
+    big = torch.full((nbytes + 16384,), 255, dtype=torch.uint8, device=gpu)
+    big[:nbytes] = dw.packed
+    y = ops.linear_f16(to_dev(x, gpu), ops.DenseWeight(big, K, N))
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    assert np.isfinite(y).all(), "the dense kernel read past the packed weight"
+    O.check_close(y, x.astype(np.float64) @ W.astype(np.float64).T, TOL, "f16 linear tail")

@@ -58,6 +58,7 @@ def test_dequant_bit_exact(gpu, sd):
 GEMV_CASES = [  # (M, K, N); the decode kernel takes M <= 8
     (1, 256, 32), (1, 4096, 4096), (5, 2560, 9216), (3, 9216, 2560), (2, 2560, 1000),
     (8, 512, 2048), (8, 1024, 300), (7, 640, 96), (1, 17408, 640), (4, 64, 33), (1, 12288, 4096),
+    (5, 4096, 6144),  # the 9B layer's stacked q/k/v
 ]
 
 
@@ -239,3 +240,24 @@ def test_reference_correctness_cases(gpu, M, K, N):
     for name, pw in (("blocked", pw_blk), ("mlx", pw_mlx)):
         y = _run(gpu, x, pw)
         O.check_close(y[:, cols], ref, TOL, f"reference case M={M} K={K} N={N} via {name}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 17408, 40), (5, 17408, 40), (1, 640, 48), (3, 2560, 33)])
+def test_gemv_reads_nothing_past_the_weight(gpu, M, K, N):
+    """A wave's last groups past K (K not a multiple of its group range) must read zeros,
+    not whatever follows the packed weight in memory: the weight sits at the head of a
+    buffer whose tail is all-ones bits (NaN as fp16 scales). A load past the range that
+    escaped the descriptor's range check would turn a zero product into NaN."""
+    import torch
+
+    from raceline_amd import ops
+
+    q, s, b = make_layer(17 + K, N, K, "f16")
+    x = make_x(3, M, K)
+    pw = upload(q, s, b, "f16", gpu)
+    nbytes = pw.packed.numel()
+    big = torch.full((nbytes + 16384,), 255, dtype=torch.uint8, device=gpu)
+    big[:nbytes] = pw.packed
+    y = _run(gpu, x, ops.PackedWeight(big, K, N, torch.float16), kernel=1)
+    assert np.isfinite(y).all(), "the decode kernel read past the packed weight"
+    O.check_close(y, O.linear_affine_f64(x, q, s, b, "f16"), TOL, f"gemv tail M={M} K={K} N={N}")

@@ -110,3 +110,27 @@ def test_native_rows_do_not_depend_on_other_rows(gpu):
     y_all = _run(gpu, x, nw, kernel=1)
     for m in (0, 5):
         np.testing.assert_array_equal(_run(gpu, x[m:m + 1], nw, kernel=1)[0], y_all[m])
+
+
+@pytest.mark.parametrize("book", BOOKS)
+def test_native_reads_nothing_past_the_weight(gpu, book):
+    """As the affine test of the same name: codes past a wave's range read zeros, never the
+    all-ones bytes that follow the packed codes in their buffer."""
+    import torch
+
+    from raceline_amd import ops
+
+    rng = np.random.default_rng(5)
+    M, K, N = 3, 17408, 40
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    s_row = rng.uniform(0.002, 0.02, size=N).astype(np.float32)
+    x = rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)
+    nw = _upload(q, s_row, book, gpu)
+    nbytes = nw.packed.numel()
+    big = torch.full((nbytes + 16384,), 255, dtype=torch.uint8, device=gpu)
+    big[:nbytes] = nw.packed
+    nw2 = ops.NativeWeight(big, nw.s_row, K, N, book)
+    for kernel in (1, 2):
+        y = _run(gpu, x, nw2, kernel=kernel)
+        assert np.isfinite(y).all(), f"kernel {kernel} read past the packed codes"
+        O.check_close(y, O.linear_native_f64(x, q, s_row, book), TOL, f"native tail {book} kernel {kernel}")

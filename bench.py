@@ -5,7 +5,9 @@
 
 Headline (BASELINE metric "4-bit GEMV achieved HBM GB/s at M=1"): one step is the
 9B-class decode layer's six projections (q, k, v, o, gate_up, down)
-at M=1, each one launch of the decode kernel, 4-bit affine g64 with fp16 scales, weights
+at M=1 as the reference's engine runs them: q, k and v stacked into one matrix (its
+attn.qkv tensor, one linear: src/engine.mm:1163-1167), so four launches of the decode
+kernel (qkv, o, gate_up, down), 4-bit affine g64 with fp16 scales, weights
 N(0, 0.02) quantized on the device and activations fp16 N(0, 1). Every step uses the next
 of >= 1 GiB of distinct weight copies so that the 256 MB Infinity Cache cannot serve
 re-reads. Steps are replayed from HIP graphs (one per copy) so that host launch cost does
@@ -14,7 +16,8 @@ not pace the GPU. value = algorithmic bytes of the step / measured time per step
 Also reported under "detail": the M=5 layer, the 27B layer at M=1 and M=8 (config 3), the
 27B prefill layer at M=2048 (config 4, TFLOP/s against the dense fp16 MFMA peak), the MoE
 layer at T=1 and T=512 (config 5), each projection's kernel time, and the CPU baseline: the reference's numpy dequant + fp32
-matmul (oracle.linear_affine_cpu_f32) on a bounded sample, timed on this host.
+matmul (oracle.linear_affine_cpu_f32) on a bounded sample, timed on this host. The
+six-launch layer (q, k, v as separate matrices) is reported under detail too.
 """
 
 from __future__ import annotations
@@ -235,13 +238,14 @@ def time_kernel(layers, shapes, M, idx, device, launches, kernel=0, outliers=0.0
 
 def cpu_baseline(device, budget_s=15.0):
     """The reference's CPU path (numpy dequant + fp32 BLAS matmul, as restated in the
-    oracle) on the 9B layer at M=1, weights copied from the GPU inputs' generator."""
+    oracle) on the 9B layer at M=1 (q/k/v stacked, as the headline), weights copied from
+    the GPU inputs' generator."""
     import numpy as np
     import torch
 
     import oracle as O
     from raceline_amd import synth
-    from raceline_amd.configs import CFG2_9B, linear_bytes
+    from raceline_amd.configs import CFG2_9B_STACKED as L9, linear_bytes
 
     try:
         from threadpoolctl import threadpool_info
@@ -249,11 +253,11 @@ def cpu_baseline(device, budget_s=15.0):
     except Exception:  # noqa: BLE001
         blas_threads = int(os.environ.get("OPENBLAS_NUM_THREADS", os.cpu_count() or 1))
     mats = []
-    for i, (_, K, N) in enumerate(CFG2_9B):
+    for i, (_, K, N) in enumerate(L9):
         w, s, b = synth.random_affine(N, K, 4242 + i, device, packed=False)
         mats.append((K, N, w.cpu().numpy().view(np.uint32), s.cpu().view(torch.int16).numpy().view(np.uint16),
                      b.cpu().view(torch.int16).numpy().view(np.uint16)))
-    x = {K: synth.random_activations(1, K, 5, device).cpu().numpy() for _, K, _ in CFG2_9B}
+    x = {K: synth.random_activations(1, K, 5, device).cpu().numpy() for _, K, _ in L9}
     total_bytes = 0
     t_deq = t_mm = 0.0
     t0 = time.perf_counter()
@@ -275,7 +279,7 @@ def cpu_baseline(device, budget_s=15.0):
     elapsed = t_deq + t_mm
     return {
         "value": total_bytes / elapsed / 1e9, "unit": "GB/s", "cores": int(blas_threads), "kind": "port",
-        "sample": f"9B decode layer (6 projections) at M=1, {reps} passes: numpy unpack+dequant "
+        "sample": f"9B decode layer (6 projections, q/k/v stacked) at M=1, {reps} passes: numpy unpack+dequant "
                   f"(1 thread) {t_deq / reps * 1e3:.1f} ms + fp32 BLAS matmul ({blas_threads} threads) "
                   f"{t_mm / reps * 1e3:.1f} ms per layer; host has {os.cpu_count()} logical CPUs",
         "ms_per_layer": elapsed / reps * 1e3,
@@ -353,7 +357,7 @@ def main():
     import torch
 
     from raceline_amd import lib
-    from raceline_amd.configs import CFG2_9B, CFG3_27B, CFG4_PREFILL_M, linear_bytes, linear_flops
+    from raceline_amd.configs import CFG2_9B, CFG2_9B_STACKED, CFG3_27B, CFG4_PREFILL_M, linear_bytes, linear_flops
 
     lib.load()
     if not torch.cuda.is_available():
@@ -361,20 +365,21 @@ def main():
     dev = torch.device("cuda:0")
     sd = torch.float16
 
-    # ---------------- headline: 9B decode layer, M = 1
-    copies = copies_for(CFG2_9B)
-    log(f"[bench] building {copies} copies of the 9B layer ({layer_bytes(CFG2_9B, 1) / 1e6:.1f} MB each)")
-    l9 = build_layer_copies(CFG2_9B, copies, 1, dev, sd)
-    run1 = LayerRunner(l9, CFG2_9B, 1, dev)
+    # ---------------- headline: 9B decode layer (q/k/v stacked), M = 1
+    L9 = CFG2_9B_STACKED
+    copies = copies_for(L9)
+    log(f"[bench] building {copies} copies of the 9B layer ({layer_bytes(L9, 1) / 1e6:.1f} MB each)")
+    l9 = build_layer_copies(L9, copies, 1, dev, sd)
+    run1 = LayerRunner(l9, L9, 1, dev)
     t1 = time_steps(run1, args.steps, args.warmup)
-    bytes1 = layer_bytes(CFG2_9B, 1)
+    bytes1 = layer_bytes(L9, 1)
     value = bytes1 / t1 / 1e9
     log(f"[bench] 9B layer M=1: {t1 * 1e6:.1f} us/step, {value:.0f} GB/s")
 
     # dominant kernel: gate_up GEMV at M=1
-    gu = [i for i, (n, _, _) in enumerate(CFG2_9B) if n == "gate_up"][0]
-    _, Kg, Ng = CFG2_9B[gu]
-    t_gu = time_kernel(l9, CFG2_9B, 1, gu, dev, launches=4 * copies)
+    gu = [i for i, (n, _, _) in enumerate(L9) if n == "gate_up"][0]
+    _, Kg, Ng = L9[gu]
+    t_gu = time_kernel(l9, L9, 1, gu, dev, launches=4 * copies)
     ach = linear_bytes(1, Kg, Ng) / t_gu / 1e9
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
@@ -384,15 +389,24 @@ def main():
     detail = {"layer_9b_m1": {"us_per_step": round(t1 * 1e6, 2), "GB/s": round(value, 1)}}
     if not args.quick:
         per = {}
-        for i, (name, K, N) in enumerate(CFG2_9B):
-            t = time_kernel(l9, CFG2_9B, 1, i, dev, launches=2 * copies)
+        for i, (name, K, N) in enumerate(L9):
+            t = time_kernel(l9, L9, 1, i, dev, launches=2 * copies)
             per[name] = {"us": round(t * 1e6, 2), "GB/s": round(linear_bytes(1, K, N) / t / 1e9, 1)}
         detail["proj_9b_m1"] = per
-        run5 = LayerRunner(l9, CFG2_9B, 5, dev)
+        run5 = LayerRunner(l9, L9, 5, dev)
         t5 = time_steps(run5, args.steps, args.warmup)
         detail["layer_9b_m5"] = {"us_per_step": round(t5 * 1e6, 2),
-                                 "GB/s": round(layer_bytes(CFG2_9B, 5) / t5 / 1e9, 1)}
+                                 "GB/s": round(layer_bytes(L9, 5) / t5 / 1e9, 1)}
         del run1, run5, l9
+        torch.cuda.empty_cache()
+        # the same layer with q, k and v as three matrices (six launches)
+        c6 = copies_for(CFG2_9B)
+        l6 = build_layer_copies(CFG2_9B, c6, 1, dev, sd)
+        r6 = LayerRunner(l6, CFG2_9B, 1, dev)
+        t6 = time_steps(r6, args.steps, args.warmup)
+        detail["layer_9b_m1_six_launches"] = {"us_per_step": round(t6 * 1e6, 2),
+                                              "GB/s": round(layer_bytes(CFG2_9B, 1) / t6 / 1e9, 1)}
+        del r6, l6
         torch.cuda.empty_cache()
 
         c27 = copies_for(CFG3_27B)
@@ -421,11 +435,12 @@ def main():
         cpu = cpu_baseline(dev)
 
     line = {
-        "metric": "4-bit GEMV achieved HBM GB/s at M=1 (9B decode layer, 6 projections)",
+        "metric": "4-bit GEMV achieved HBM GB/s at M=1 (9B decode layer, 6 projections, q/k/v stacked)",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(t1 * 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic (seeded N(0,0.02) weights quantized on device, fp16 N(0,1) activations)",
-        "config": {"workload": "9B-class decode layer projections q,k,v,o,gate_up,down; 4-bit affine g64, "
+        "config": {"workload": "9B-class decode layer projections q,k,v (one stacked matrix, as the "
+                               "reference's attn.qkv),o,gate_up,down; 4-bit affine g64, "
                                "fp16 scales+biases, M=1, fp32 accumulate", "global_batch": 1, "seq_len": 1,
                    "parallelism": "single GPU", "weight_copies": copies, "bytes_per_step": bytes1},
         "roofline": roofline,

@@ -8,6 +8,11 @@ CFG1_SINGLE = [("linear", 4096, 4096)]                                   # M = 1
 CFG2_9B = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
            ("gate_up", 4096, 24576), ("down", 12288, 4096)]               # M in {1, 5}
 
+# The same layer as the reference's engine runs it: q, k and v stacked into one matrix
+# (the model file's attn.qkv with parts q, k, v; one linear over it, src/engine.mm:1163-1167).
+CFG2_9B_STACKED = [("qkv", 4096, 4096 + 2 * 1024), ("o", 4096, 4096), ("gate_up", 4096, 24576),
+                   ("down", 12288, 4096)]                                # M in {1, 5}
+
 CFG3_27B = [("qkv", 5120, 5120 + 2 * 1024), ("o", 5120, 5120), ("gate_up", 5120, 34816),
             ("down", 17408, 5120)]                                        # M in {1, 8}
 

@@ -383,7 +383,7 @@ def main():
     ach = linear_bytes(1, Kg, Ng) / t_gu / 1e9
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                "kernel": "gemv_q4a_kernel<1,16,0,false> (9B gate_up, M=1, K=4096, N=24576)",
+                "kernel": "gemv_q4a_kernel<1,8,0,false,0> (9B gate_up, M=1, K=4096, N=24576)",
                 "avg_launch_us": round(t_gu * 1e6, 2), "algorithmic_bytes": linear_bytes(1, Kg, Ng)}
 
     detail = {"layer_9b_m1": {"us_per_step": round(t1 * 1e6, 2), "GB/s": round(value, 1)}}

@@ -162,7 +162,7 @@ __global__ void dequant_kernel(const u32x4 *codes, const u32x4 *sb, int K, int N
 // ================================================================== decode GEMV (M <= 8)
 //
 // Grid: one workgroup per tile of 16 output features; W = ceil(groups / GPW) waves (at
-// most 16; GPW in {16, 24} groups per wave, a function of K only) split the K groups into
+// most 16; GPW in {8, 12, 16, 24} groups per wave, a function of K only) split the K groups into
 // consecutive ranges, and their partial sums meet in LDS in wave order. No split of K
 // across workgroups: every output is written by the workgroup that owns it, and the
 // order of every sum depends only on K, never on M or on timing, so a token's result is
@@ -193,8 +193,14 @@ struct GemvArgs {
   int x_stride, M, K, N, y_stride;
 };
 
-// Groups per wave: 16, or 24 when 16 would need more than 16 waves.
-static int gemv_gpw(int K) { return 4 * quads_of(K) <= 16 * 16 ? 16 : 24; }
+// Groups per wave: the smallest of 8, 12, 16, 24 that needs at most 16 waves. Smaller
+// ranges put more waves (and more loads) in flight per tile; below 8 the per-wave setup
+// and the cross-wave reduction cost more than they hide (measured on the 9B and 27B
+// projections at M = 1, 5, 8).
+static int gemv_gpw(int K) {
+  const int g = 4 * quads_of(K);
+  return g <= 8 * 16 ? 8 : g <= 12 * 16 ? 12 : g <= 16 * 16 ? 16 : 24;
+}
 static int gemv_waves(int K) { const int g = gemv_gpw(K); return (4 * quads_of(K) + g - 1) / g; }
 
 // the cross-wave reduction [waves-1][64][4] floats, then (M = 1) each wave's staged
@@ -345,10 +351,14 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
   const dim3 grid(tiles_of(N));
   const int threads = 64 * waves;
   int rc;
-  if (M == 1) rc = gpw == 16 ? launch_gemv<1, 16>(book, sd, accum, grid, threads, lds, st, a)
-                             : launch_gemv<1, 24>(book, sd, accum, grid, threads, lds, st, a);
-  else rc = gpw == 16 ? launch_gemv<kGemvMaxM, 16>(book, sd, accum, grid, threads, lds, st, a)
-                      : launch_gemv<kGemvMaxM, 24>(book, sd, accum, grid, threads, lds, st, a);
+  if (M == 1) rc = gpw == 8    ? launch_gemv<1, 8>(book, sd, accum, grid, threads, lds, st, a)
+                   : gpw == 12 ? launch_gemv<1, 12>(book, sd, accum, grid, threads, lds, st, a)
+                   : gpw == 16 ? launch_gemv<1, 16>(book, sd, accum, grid, threads, lds, st, a)
+                               : launch_gemv<1, 24>(book, sd, accum, grid, threads, lds, st, a);
+  else rc = gpw == 8    ? launch_gemv<kGemvMaxM, 8>(book, sd, accum, grid, threads, lds, st, a)
+            : gpw == 12 ? launch_gemv<kGemvMaxM, 12>(book, sd, accum, grid, threads, lds, st, a)
+            : gpw == 16 ? launch_gemv<kGemvMaxM, 16>(book, sd, accum, grid, threads, lds, st, a)
+                        : launch_gemv<kGemvMaxM, 24>(book, sd, accum, grid, threads, lds, st, a);
   if (rc) return rc;
   RLQ_HIP(hipGetLastError());
   return 0;

@@ -204,6 +204,35 @@ def bench_moe(device, steps, warmup):
     return out
 
 
+def bench_prefill(device, steps, warmup):
+    """the 27B layer's four projections at M = 2048 (fp16 activations with
+    1% outliers x20), TFLOP/s against the dense fp16 MFMA peak; two weight copies."""
+    import torch
+
+    from raceline_amd.configs import CFG3_27B, CFG4_PREFILL_M, linear_flops
+
+    l27 = build_layer_copies(CFG3_27B, 2, 2, device, torch.float16)
+    rp = LayerRunner(l27, CFG3_27B, CFG4_PREFILL_M, device, outliers=0.01)
+    tp = time_steps(rp, max(4, steps // 5), 2)
+    flops = sum(linear_flops(CFG4_PREFILL_M, K, N) for _, K, N in CFG3_27B)
+    log(f"[bench] 27B prefill: {flops / tp / 1e12:.1f} TFLOP/s")
+    del rp, l27
+    torch.cuda.empty_cache()
+    return {"prefill_27b_m2048": {"us_per_step": round(tp * 1e6, 1), "TFLOP/s": round(flops / tp / 1e12, 1),
+                                  "frac_of_mfma_peak": round(flops / tp / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}}
+
+
+def bench_part(part, steps, warmup):
+    import torch
+
+    from raceline_amd import lib
+
+    lib.load()
+    dev = torch.device("cuda:0")
+    log(f"[bench] part {part}")
+    return bench_prefill(dev, steps, warmup) if part == "prefill" else bench_moe(dev, steps, warmup)
+
+
 def time_kernel(layers, shapes, M, idx, device, launches, kernel=0, outliers=0.0):
     """Average duration of projection idx's kernel: a captured graph of `launches`
     back-to-back launches over the rotating copies, replayed between two events on the
@@ -340,6 +369,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail configs, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--part", choices=["prefill", "moe"],
+                    help="run only this part of the detail (for rocprofv3); prints its figures as JSON")
     ap.add_argument("--profile", action="store_true",
                     help="launch only the dominant kernel and a calibration kernel (for rocprofv3)")
     args = ap.parse_args()
@@ -353,11 +384,14 @@ def main():
     if args.profile:
         profile_dominant(max(args.steps, 40))
         return
+    if args.part:
+        print(json.dumps(bench_part(args.part, args.steps, args.warmup)), flush=True)
+        return
 
     import torch
 
     from raceline_amd import lib
-    from raceline_amd.configs import CFG2_9B, CFG2_9B_STACKED, CFG3_27B, CFG4_PREFILL_M, linear_bytes, linear_flops
+    from raceline_amd.configs import CFG2_9B, CFG2_9B_STACKED, CFG3_27B, linear_bytes
 
     lib.load()
     if not torch.cuda.is_available():
@@ -418,15 +452,10 @@ def main():
             detail[f"layer_27b_m{M}"] = {"us_per_step": round(t * 1e6, 2),
                                          "GB/s": round(layer_bytes(CFG3_27B, M) / t / 1e9, 1)}
             del r
-        # prefill: M = 2048, compute bound; two copies are plenty
-        rp = LayerRunner(l27[:2], CFG3_27B, CFG4_PREFILL_M, dev, outliers=0.01)
-        tp = time_steps(rp, max(4, args.steps // 5), 2)
-        flops = sum(linear_flops(CFG4_PREFILL_M, K, N) for _, K, N in CFG3_27B)
-        detail["prefill_27b_m2048"] = {"us_per_step": round(tp * 1e6, 1), "TFLOP/s": round(flops / tp / 1e12, 1),
-                                       "frac_of_mfma_peak": round(flops / tp / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
-        log(f"[bench] 27B prefill: {flops / tp / 1e12:.1f} TFLOP/s")
-        del rp, l27
+        del l27
         torch.cuda.empty_cache()
+        # prefill: M = 2048, compute bound; two copies are plenty
+        detail.update(bench_prefill(dev, args.steps, args.warmup))
         detail.update(bench_moe(dev, args.steps, args.warmup))
 
     cpu = None

@@ -76,6 +76,10 @@ class LayerRunner:
         # grow the workspace to its largest size before capture (no allocation inside a graph)
         for (_, K, N) in shapes:
             ops._WS.get(device, ops.workspace_bytes(M, K, N))
+        # The buffers above come from the default stream's allocator pool, whose blocks may
+        # still be written by kernels queued there (weight generation, freed temporaries):
+        # the side stream starts only when that work is done.
+        torch.cuda.synchronize()
         self.stream = torch.cuda.Stream()
         with torch.cuda.stream(self.stream):
             for c in range(len(layers)):
@@ -136,6 +140,11 @@ class StepGraphs:
         import torch
 
         self.torch = torch
+        # The step's buffers come from the default stream's allocator pool, whose blocks may
+        # still be written by kernels queued there (weight generation, freed temporaries).
+        # The MoE step computes addresses from the routing tables it writes into such a
+        # block: without this wait a queued kernel can overwrite them under the side stream.
+        torch.cuda.synchronize()
         self.stream = torch.cuda.Stream()
         with torch.cuda.stream(self.stream):
             for fn in steps_per_copy:
@@ -245,6 +254,7 @@ def time_kernel(layers, shapes, M, idx, device, launches, kernel=0, outliers=0.0
     x = synth.random_activations(M, K, 99, device, outliers)
     y = torch.empty((M, N), dtype=torch.float32, device=device)
     ops._WS.get(device, ops.workspace_bytes(M, K, N))
+    torch.cuda.synchronize()          # x, y and the workspace are ready before the side stream uses them
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         for c in range(len(layers)):

@@ -228,6 +228,31 @@ __device__ __forceinline__ f32x4 tile_dot_rows(const WaveTile &w, __amdgpu_buffe
   return acc;
 }
 
+// The wave's part of a 16-row weight tile (its loads already issued into wq, sq) times 16
+// token rows staged in LDS in operand order: xs points at row 0's element 64 * wg0 (the
+// wave's first group), rows rstride halves apart. Lane (c16, j4) reads row c16.
+template <int GPW, int SD, int BOOK = kAffine>
+__device__ __forceinline__ f32x4 tile_dot_lds(const u32x4 (&wq)[GPW / 2], const u32x4 (&sq)[GPW / 4],
+                                              const _Float16 *xs, int rstride, int wn, int lane) {
+  const _Float16 *xa = xs + (lane & 15) * rstride + 8 * (lane >> 4);
+  f32x4 acc = {}, asum = {};
+#pragma unroll
+  for (int jg = 0; jg < GPW; ++jg) {
+    if (jg < wn) {   // uniform: the groups past the wave's range add nothing
+      half8 af[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(xa + jg * kGroup + 32 * s);
+      book_step<GPW, SD, 4, BOOK>(acc, asum, af, wq, sq, jg);
+      asm volatile("" : "+v"(acc));
+    }
+  }
+  if constexpr (BOOK == kInt16) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(0.5f, asum[v], acc[v]);
+  }
+  return acc;
+}
+
 // Waves 1.. of the workgroup hand their partials to wave 0, which adds them in wave order
 // (a fixed order: the result depends only on the number of waves). red: (waves-1)*64
 // f32x4 of LDS. Returns the total in wave 0 (other waves' return value is unspecified).

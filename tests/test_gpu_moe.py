@@ -181,3 +181,25 @@ def test_layer_full_size_batch_invariance(gpu):
             ref[i] += w[i * S + s] * O.linear_affine_f64(a.astype(np.float64), O.unpack_nibbles_u32(wd[rd]), sd_[rd],
                                                          bd[rd])[0]
     O.check_close(h.cpu().numpy()[toks].astype(np.float64), ref, TOL, "moe full-size sampled tokens")
+
+
+def test_token_result_same_across_kernel_choice(gpu):
+    """Calls of fewer than 8 tokens run the per-tile expert kernel, larger ones the kernel
+    that stages each item's rows in LDS; a token's result must not depend on which one
+    ran: tokens 3..7 alone (per-tile) give the same bits as inside a 40-token call."""
+    import torch
+
+    from raceline_amd import ops
+
+    E, topk, H, I = 64, 8, 2048, 512
+    gu, dn = make_moe(90, E, H, I)
+    mw = upload_moe(gu, dn, E, H, I, "f16", gpu)
+    x, logits = make_inputs(91, 40, E, H)
+    h = torch.zeros((40, H), dtype=torch.float32, device=gpu)
+    ops.moe(to_dev(x, gpu), to_dev(logits, gpu), mw, topk, h)
+    h5 = torch.zeros((5, H), dtype=torch.float32, device=gpu)
+    ops.moe(to_dev(x[3:8].copy(), gpu), to_dev(logits[3:8].copy(), gpu), mw, topk, h5)
+    _sync()
+    assert torch.equal(h5, h[3:8])
+    ref, _, _ = O.moe_layer_f64(x[3:8], logits[3:8], gu, dn, E, topk, I, H)
+    O.check_close(h5.cpu().numpy().astype(np.float64), ref, TOL, "moe per-tile vs staged")

@@ -338,7 +338,7 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
     for (int st = 0; st < steps; ++st) {
       const int q = 2 * st + h;                      // quad of groups 4q .. 4q+3
       const u32x4 v = q < G4 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             rs, (uint32_t)tt * G4 * 256u + 16u * cr, (uint32_t)q * 256u, 0))
+                                                             rs, (uint32_t)tt * G4 * 256u + (uint32_t)q * 256u + 16u * cr, 0, 0))
                              : u32x4{};
       u32x4 d;
 #pragma unroll

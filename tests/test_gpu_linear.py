@@ -59,6 +59,7 @@ GEMV_CASES = [  # (M, K, N); the decode kernel takes M <= 8
     (1, 256, 32), (1, 4096, 4096), (5, 2560, 9216), (3, 9216, 2560), (2, 2560, 1000),
     (8, 512, 2048), (8, 1024, 300), (7, 640, 96), (1, 17408, 640), (4, 64, 33), (1, 12288, 4096),
     (5, 4096, 6144),  # the 9B layer's stacked q/k/v
+    (1, 64, 16), (3, 320, 40), (8, 576, 17),  # one group; odd group counts
 ]
 
 
@@ -83,7 +84,9 @@ def test_gemv_accumulates(gpu, M, K, N):
 
 
 GEMM_CASES = [(9, 512, 96), (16, 1024, 300), (32, 2048, 1024), (33, 256, 64), (130, 5120, 1024),
-              (512, 2048, 1024), (70, 9216, 2560), (256, 1024, 300), (40, 2560, 1000)]
+              (512, 2048, 1024), (70, 9216, 2560), (256, 1024, 300), (40, 2560, 1000),
+              # an odd number of groups (the last pair half empty), a single group, ragged M and N
+              (129, 320, 17), (64, 64, 48), (200, 576, 272), (300, 192, 513)]
 
 
 @pytest.mark.parametrize("M,K,N", GEMM_CASES)

@@ -395,17 +395,16 @@ size_t gemm4_workspace(int book, int M, int K) {
 }
 
 template <int BOOK, int SD>
-static void launch_gemm4_inst(int accum, dim3 grid, size_t lds, hipStream_t st, const GemmArgs &a) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm4_kernel<BOOK, SD, true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm4_kernel<BOOK, SD, false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    attr_set = true;
+static int launch_gemm4_inst(int accum, dim3 grid, size_t lds, hipStream_t st, const GemmArgs &a) {
+  static LdsOptIn lds_acc, lds_set;
+  if (accum) {
+    if (int rc = allow_large_lds(reinterpret_cast<const void *>(&gemm4_kernel<BOOK, SD, true>), lds_acc)) return rc;
+    gemm4_kernel<BOOK, SD, true><<<grid, kGThreads, lds, st>>>(a);
+  } else {
+    if (int rc = allow_large_lds(reinterpret_cast<const void *>(&gemm4_kernel<BOOK, SD, false>), lds_set)) return rc;
+    gemm4_kernel<BOOK, SD, false><<<grid, kGThreads, lds, st>>>(a);
   }
-  if (accum) gemm4_kernel<BOOK, SD, true><<<grid, kGThreads, lds, st>>>(a);
-  else gemm4_kernel<BOOK, SD, false><<<grid, kGThreads, lds, st>>>(a);
+  return 0;
 }
 
 int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
@@ -444,14 +443,16 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
   const int mblocks = (M + kGM - 1) / kGM, nblocks = (N + kGN - 1) / kGN;
   const dim3 grid(mblocks * nblocks);
   const size_t lds = (size_t)kStages * kStageBytes;
+  int rc;
   switch (book) {
-    case kInt15: launch_gemm4_inst<kInt15, 0>(accum, grid, lds, st, a); break;
-    case kInt16: launch_gemm4_inst<kInt16, 0>(accum, grid, lds, st, a); break;
-    case kFp4: launch_gemm4_inst<kFp4, 0>(accum, grid, lds, st, a); break;
+    case kInt15: rc = launch_gemm4_inst<kInt15, 0>(accum, grid, lds, st, a); break;
+    case kInt16: rc = launch_gemm4_inst<kInt16, 0>(accum, grid, lds, st, a); break;
+    case kFp4: rc = launch_gemm4_inst<kFp4, 0>(accum, grid, lds, st, a); break;
     default:
-      if (sd == RLQ_BF16) launch_gemm4_inst<kAffine, 1>(accum, grid, lds, st, a);
-      else launch_gemm4_inst<kAffine, 0>(accum, grid, lds, st, a);
+      rc = sd == RLQ_BF16 ? launch_gemm4_inst<kAffine, 1>(accum, grid, lds, st, a)
+                          : launch_gemm4_inst<kAffine, 0>(accum, grid, lds, st, a);
   }
+  if (rc) return rc;
   RLQ_HIP(hipGetLastError());
   return 0;
 }

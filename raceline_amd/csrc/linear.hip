@@ -301,12 +301,9 @@ static size_t gemv_workspace(int, int, int) { return 0; }
 
 template <int MAXM, int GPW, int SD, bool ACC, int BOOK>
 static int launch_gemv_inst(dim3 grid, int threads, size_t lds, hipStream_t st, const GemvArgs &a) {
-  static bool attr_set = false;  // once per instance, before its first launch
-  if (!attr_set) {
-    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4a_kernel<MAXM, GPW, SD, ACC, BOOK>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    attr_set = true;
-  }
+  static LdsOptIn lds_opt;  // per instance and device, before its first launch there
+  if (int rc = allow_large_lds(reinterpret_cast<const void *>(&gemv_q4a_kernel<MAXM, GPW, SD, ACC, BOOK>), lds_opt))
+    return rc;
   gemv_q4a_kernel<MAXM, GPW, SD, ACC, BOOK><<<grid, threads, lds, st>>>(a);
   return 0;
 }

@@ -416,18 +416,14 @@ static int launch_staged_inst(int tpe, hipStream_t st, MoeArgs a, int items) {
   const int xpt = (chunks + threads - 1) / threads;
   const size_t lds = (size_t)16 * (a.K + 8) * 2 + (size_t)tpb * (W - 1) * 64 * 16;
   const dim3 grid((tpe + tpb - 1) / tpb, items);
-  static bool attr_set = false;
-  if (!attr_set) {
-    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    attr_set = true;
-  }
+  static LdsOptIn lds_opt[4];
+  const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8>)};
+  const int which = xpt <= 1 ? 0 : xpt <= 2 ? 1 : xpt <= 4 ? 2 : 3;
+  if (xpt <= 8)
+    if (int rc = allow_large_lds(fns[which], lds_opt[which])) return rc;
   if (xpt <= 1) moe_expert_lds_kernel<GPW, SD, KIND, 1><<<grid, threads, lds, st>>>(a);
   else if (xpt <= 2) moe_expert_lds_kernel<GPW, SD, KIND, 2><<<grid, threads, lds, st>>>(a);
   else if (xpt <= 4) moe_expert_lds_kernel<GPW, SD, KIND, 4><<<grid, threads, lds, st>>>(a);
@@ -495,12 +491,8 @@ int rlq_moe_route(const float *logits, int logit_stride, int T, int E, int topk,
   RLQ_HIP(hipGetLastError());
   const int wpe = sort_wpe(E);
   const size_t lds = sort_lds_bytes(E, wpe);
-  static bool attr_set = false;
-  if (!attr_set) {
-    RLQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_sort_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    attr_set = true;
-  }
+  static LdsOptIn lds_opt;
+  if (int rc = allow_large_lds(reinterpret_cast<const void *>(&moe_sort_kernel), lds_opt)) return rc;
   moe_sort_kernel<<<1, 1024, lds, st>>>(sel, T, E, topk + 1, wpe, tok, inv, reinterpret_cast<int4 *>(items), n_items);
   RLQ_HIP(hipGetLastError());
   return 0;

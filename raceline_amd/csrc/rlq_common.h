@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstddef>
 #include <cstdint>
@@ -32,6 +33,14 @@ int check_hip(hipError_t e, const char *what);
   } while (0)
 
 inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Lets a kernel use up to 160 KB of dynamic LDS on the current device. A function
+// attribute belongs to one device, so every device is set once; `done` is the call site's
+// record of the devices already set (bit d: device d; devices past 63 are set every call).
+struct LdsOptIn {
+  std::atomic<uint64_t> done{0};
+};
+int allow_large_lds(const void *fn, LdsOptIn &done);
 
 // ----------------------------------------------------------------- device helpers
 

@@ -1,4 +1,5 @@
-// Library-level entry points: error mode, last error, device selection, workspace clearing.
+// Library-level entry points (error mode, last error, device selection) and the runtime
+// helpers the kernels' launchers share.
 #include "rlq_common.h"
 #include "../../include/rlq.h"
 
@@ -29,6 +30,16 @@ int fail(const char *fmt, ...) {
 int check_hip(hipError_t e, const char *what) {
   if (e == hipSuccess) return 0;
   return fail("%s: %s", what, hipGetErrorString(e));
+}
+
+int allow_large_lds(const void *fn, LdsOptIn &done) {
+  int dev = 0;
+  RLQ_HIP(hipGetDevice(&dev));
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit && (done.done.load(std::memory_order_acquire) & bit)) return 0;
+  RLQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  if (bit) done.done.fetch_or(bit, std::memory_order_acq_rel);
+  return 0;
 }
 
 }  // namespace rlq

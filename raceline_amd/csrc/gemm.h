@@ -15,7 +15,6 @@ struct GemmArgs {
   const float *asum;    // kInt16: activation row sums [M]
   float *y;
   int x_stride, M, K, N, y_stride, gs_stride;
-  uint32_t magic;       // 0x64006400, the fp16 exponent pattern of 1024 in both halves
 };
 
 // Bytes of workspace run_gemm4 needs (affine: the prepped activations and the split group

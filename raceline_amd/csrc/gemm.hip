@@ -11,8 +11,8 @@
 //    (buffer_load ... lds: no registers, no VALU) two pairs ahead of use. Activation rows
 //    are stored with their 16-byte chunks XOR-swizzled by the row, so the MFMA operand
 //    reads hit distinct banks.
-//  - Codes become exact fp16 values in registers (bit-field insert under the exponent of
-//    1024, minus 1024).
+//  - Codes become exact fp16 subnormals q * 2^-24 in registers (four masks and a shift per
+//    eight codes: the operand trick of q4_tile.h), the scale carries the 2^24.
 //  - The 32 MFMAs of a pair run in a fixed order with each A fragment read from LDS 8
 //    MFMAs ahead; affine group products are scaled into the fp32 accumulators by FMAs
 //    interleaved with the MFMAs of the next half-group.
@@ -39,36 +39,6 @@ constexpr int kBBytes = (kGN / 16) * 1024;  // stage part: the 16 tiles' code ki
 constexpr int kSBytes = (kGN / 16) * 256;   // stage part: their scale/bias quads, 4 KB
 constexpr int kStageBytes = kABytes + kBBytes + kSBytes;
 constexpr int kStages = 3;                  // loads run two group pairs ahead of the MFMAs
-
-// (1024 + a, 1024 + b) as fp16 bits -> exactly (a, b)
-__device__ __forceinline__ uint32_t sub1024_pair(uint32_t bits) {
-  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-  const half2v m = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, bits) + m);
-}
-
-// (mask & a) | (~mask & b) in one v_bfi_b32. Written out because the compiler splits the
-// pattern into an and + or pair when the mask is a literal (gfx950's VOP3 encoding takes
-// no literal operand); here the mask sits in a scalar register.
-__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
-  return r;
-}
-
-// Eight codes (oddx16 element order of q4_tile.h) -> exact normal fp16: (q0, q4),
-// (16 q1, 16 q5), (q2, q6), (16 q3, 16 q7). Nine ops: each pair of codes is inserted under
-// the exponent pattern of 1024 (mg = 0x64006400, kept in a vector register) with one
-// v_bfi_b32, and 1024 is subtracted.
-__device__ __forceinline__ half8 nib8_to_half8_oddx16_exact(uint32_t u, uint32_t mg) {
-  const uint32_t t = u >> 8;
-  u32x4 d;
-  d[0] = sub1024_pair(bfi(0x000F000Fu, u, mg));
-  d[1] = sub1024_pair(bfi(0x00F000F0u, u, mg));
-  d[2] = sub1024_pair(bfi(0x000F000Fu, t, mg));
-  d[3] = sub1024_pair(bfi(0x00F000F0u, t, mg));
-  return __builtin_bit_cast(half8, d);
-}
 
 // ------------------------------------------------------------------ affine prep pass
 
@@ -286,11 +256,11 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
       // (past the last pair the carried reads see a stale stage, and are not used)
       if (j + 8 < 32) fr[j + 8] = read_frag(lds, stage, aoff, j + 8);
       else carry[j - 24] = read_frag(lds, (p + 1) % kStages, aoff, j - 24);
-      if ((j & 15) == 0 && BOOK == kAffine) sc = scale_f32<SD>((uint16_t)(sp[gg] & 0xFFFFu));
+      if ((j & 15) == 0 && BOOK == kAffine) sc = scale_f32<SD>((uint16_t)(sp[gg] & 0xFFFFu)) * kTwo24;
       if ((j & 15) < 8 && t == 0) {
         // codes of step i, group gg: word 2i + h, i.e. read (i & 1), element 2 gg + (i >> 1)
         const uint32_t u = wq[i & 1][2 * gg + (i >> 1)];
-        if constexpr (BOOK == kAffine) bf[i] = nib8_to_half8_oddx16_exact(u, a.magic);
+        if constexpr (BOOK == kAffine) bf[i] = nib8_to_half8_oddx16(u);
         else bf[i] = native8_to_half8<BOOK>(u);
       }
       if constexpr (BOOK == kAffine) {
@@ -415,7 +385,6 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
   RLQ_REQUIRE(need == 0 || aligned(ws, 256), "workspace must be 256-byte aligned");
   RLQ_REQUIRE((size_t)M * std::max(x_stride, K) * 2 < (1ull << 31), "prefill kernel: x spans more than 2 GiB");
   GemmArgs a = {};
-  a.magic = 0x64006400u;
   a.codes = static_cast<const u32x4 *>(packed);
   a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
   a.srow = srow;

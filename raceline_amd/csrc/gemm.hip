@@ -87,29 +87,40 @@ __device__ __forceinline__ __attribute__((address_space(3))) void *lds_at(unsign
   return (__attribute__((address_space(3))) void *)(lds + (size_t)stage * kStageBytes + off);
 }
 
-// Loads group pair p into LDS stage `stage`: 4 activation chunks (16 bytes each; inputs
-// past K and rows past M read zero), 2 code chunks of 16 bytes (tile 2 wave + i: its pair-p
-// kilobyte) and 2 scale words (quad p/2 of the same tiles).
+// Loads group pair p into LDS stage `stage`: 4 activation chunks (16 bytes each), 2 code
+// chunks of 16 bytes (tile 2 wave + i: its pair-p kilobyte) and 2 scale words (quad p/2 of
+// the same tiles). The per-lane part of each offset goes in the range-checked vector
+// operand: rows past M and tiles past N read zeros. The pair's part, the same for every
+// lane, goes in the scalar operand (no ALU work), which the range check does not see; so
+// a pair reaching past K (an odd number of groups) takes the path with the whole offset
+// checked, where inputs past K read zeros.
 __device__ __forceinline__ void issue_stage(const StageSrc &s, unsigned char *lds, int p, int stage) {
+  if (128 * (p + 1) <= s.K) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 4 * (4 * s.wave + i) + (s.lane >> 4);
-    const int c = (s.lane & 15) ^ (r & 15);
-    const bool ok = s.a_row[i] && 128 * p + 8 * c < s.K;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, stage, (4 * s.wave + i) * 1024), 16,
-                                             ok ? s.a_off[i] + (uint32_t)(256 * p) : kFarOffset, 0, 0, 0);
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, stage, (4 * s.wave + i) * 1024), 16, s.a_off[i],
+                                               256 * p, 0, 0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * (4 * s.wave + i) + (s.lane >> 4);
+      const int c = (s.lane & 15) ^ (r & 15);
+      const bool ok = s.a_row[i] && 128 * p + 8 * c < s.K;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, stage, (4 * s.wave + i) * 1024), 16,
+                                               ok ? s.a_off[i] + (uint32_t)(256 * p) : kFarOffset, 0, 0, 0);
+    }
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int k = 2 * s.wave + i;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rcode, lds_at(lds, stage, kABytes + k * 1024), 16,
-                                             (uint32_t)k * s.GP * 1024u + (uint32_t)p * 1024u + 16u * s.lane, 0, 0, 0);
+                                             (uint32_t)k * s.GP * 1024u + 16u * s.lane, p * 1024, 0, 0);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int k = 2 * s.wave + i;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rsb, lds_at(lds, stage, kABytes + kBBytes + k * 256), 4,
-                                             (uint32_t)k * s.G4 * 256u + (uint32_t)(p >> 1) * 256u + 4u * s.lane, 0, 0, 0);
+                                             (uint32_t)k * s.G4 * 256u + 4u * s.lane, (p >> 1) * 256, 0, 0);
   }
 }
 

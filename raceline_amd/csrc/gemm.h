@@ -14,12 +14,15 @@ struct GemmArgs {
   const float *srow;    // native books: row scales [N]
   const float *asum;    // kInt16: activation row sums [M]
   float *y;
+  float *y_part;        // split K: the second half's partial products [M][y_part_stride]
   int x_stride, M, K, N, y_stride, gs_stride;
+  int np_first;         // split K: group pairs of the first half (all of them when not split)
+  int y_part_stride;
 };
 
 // Bytes of workspace run_gemm4 needs (affine: the prepped activations and the split group
-// sums; kInt16: group and row sums; other books: none).
-size_t gemm4_workspace(int book, int M, int K);
+// sums; kInt16: group and row sums; a shape whose K is split: the second half's partials).
+size_t gemm4_workspace(int book, int M, int K, int N);
 
 int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
               const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st);

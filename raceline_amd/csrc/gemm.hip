@@ -127,9 +127,9 @@ __device__ __forceinline__ void issue_stage(const StageSrc &s, unsigned char *ld
 
 // The B reads of a pair (two 16-byte code slots) and, affine, its two scale words.
 template <int BOOK>
-__device__ __forceinline__ void read_pair_head(const unsigned char *lds, uint32_t boff, uint32_t soff, int p,
-                                               u32x4 (&wq)[2], uint32_t (&sp)[2]) {
-  const unsigned char *base = lds + (size_t)(p % kStages) * kStageBytes;
+__device__ __forceinline__ void read_pair_head(const unsigned char *lds, uint32_t boff, uint32_t soff, int stage,
+                                               int p, u32x4 (&wq)[2], uint32_t (&sp)[2]) {
+  const unsigned char *base = lds + (size_t)stage * kStageBytes;
   wq[0] = *reinterpret_cast<const u32x4 *>(base + boff);
   wq[1] = *reinterpret_cast<const u32x4 *>(base + boff + 512);
   if constexpr (BOOK == kAffine) {
@@ -157,6 +157,15 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   const int G = a.K / kGroup, G4 = quads_of(a.K), GP = 2 * G4;
   const int NP = (G + 1) / 2;                        // group pairs with real groups
   const int T = tiles_of(a.N);
+  // Split K (gridDim.y == 2): the first half of the pairs adds the bias term and writes y
+  // (accumulating when asked); the second writes its partial products to y_part, which a
+  // second kernel adds to y, so the two halves always meet in the same order.
+  const int split = blockIdx.y;
+  const int pb = split == 0 ? 0 : a.np_first;
+  const int NPs = split == 0 ? a.np_first : NP - a.np_first;
+  float *const yout = split == 0 ? a.y : a.y_part;
+  const int ystride = split == 0 ? a.y_stride : a.y_part_stride;
+  const bool acc_here = ACC && split == 0;
 
   // Workgroups are numbered round-robin over the 8 XCDs; give each XCD a contiguous
   // range of tiles, token blocks fastest, so the workgroups of one XCD share feature
@@ -236,18 +245,18 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   // Every stage issue loads a real pair: past the last pair the index is clamped (a
   // duplicate of the last pair into a stage nobody reads any more), so exactly two
   // stages are always in flight and one wait count fits every hand-over.
-  issue_stage(src, lds, 0, 0);
-  issue_stage(src, lds, min(1, NP - 1), 1);
+  issue_stage(src, lds, pb, 0);
+  issue_stage(src, lds, pb + min(1, NPs - 1), 1);
   __builtin_amdgcn_s_waitcnt(0x0F78);                     // vmcnt(8): stage 0 in place, 1 may fly
   asm volatile("s_barrier" ::: "memory");
-  issue_stage(src, lds, min(2, NP - 1), 2);
-  read_pair_head<BOOK>(lds, boff, soff, 0, wq, sp);
+  issue_stage(src, lds, pb + min(2, NPs - 1), 2);
+  read_pair_head<BOOK>(lds, boff, soff, 0, pb, wq, sp);
 #pragma unroll
   for (int j = 0; j < 8; ++j) carry[j] = read_frag(lds, 0, aoff, j);
 
-  for (int p = 0; p < NP; ++p) {
-    const int stage = p % kStages;
-    const bool more = p + 1 < NP;
+  for (int q = 0; q < NPs; ++q) {
+    const int stage = q % kStages;
+    const bool more = q + 1 < NPs;
     half8 fr[32];
 #pragma unroll
     for (int j = 0; j < 8; ++j) fr[j] = carry[j];
@@ -261,12 +270,13 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
         // and stage p + 1 has landed for every wave
         __builtin_amdgcn_s_waitcnt(0x0078);                   // lgkmcnt(0) vmcnt(8): stage p + 2 may fly
         asm volatile("s_barrier" ::: "memory");
-        issue_stage(src, lds, min(p + 3, NP - 1), (p + 3) % kStages);
-        read_pair_head<BOOK>(lds, boff, soff, p + 1, wq, sp);   // the last codes of pair p were read at step 22
+        issue_stage(src, lds, pb + min(q + 3, NPs - 1), (q + 3) % kStages);
+        // the last codes of this pair were read at step 22
+        read_pair_head<BOOK>(lds, boff, soff, (q + 1) % kStages, pb + q + 1, wq, sp);
       }
       // (past the last pair the carried reads see a stale stage, and are not used)
       if (j + 8 < 32) fr[j + 8] = read_frag(lds, stage, aoff, j + 8);
-      else carry[j - 24] = read_frag(lds, (p + 1) % kStages, aoff, j - 24);
+      else carry[j - 24] = read_frag(lds, (q + 1) % kStages, aoff, j - 24);
       if ((j & 15) == 0 && BOOK == kAffine) sc = scale_f32<SD>((uint16_t)(sp[gg] & 0xFFFFu)) * kTwo24;
       if ((j & 15) < 8 && t == 0) {
         // codes of step i, group gg: word 2i + h, i.e. read (i & 1), element 2 gg + (i >> 1)
@@ -306,7 +316,7 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
     }
   }
 
-  if constexpr (BOOK == kAffine) {
+  if (BOOK == kAffine && split == 0) {
     // acc += sum_g b[n][g] * gsum[m][g]: an MFMA product over K' = 2G, the group sums as
     // (hi, lo) pairs. Step st covers k' = 16 st .. +15; lane half h holds k' 16 st + 8 h
     // .. +7, i.e. the (hi, lo) of groups 8 st + 4 h .. +3: b of those groups, each twice.
@@ -356,10 +366,12 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
       const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
       if (m < a.M) {
         float val = acc[mt][v];
-        if constexpr (BOOK == kInt16) val = __builtin_fmaf(0.5f, a.asum[m], val);
+        if constexpr (BOOK == kInt16) {
+          if (split == 0) val = __builtin_fmaf(0.5f, a.asum[m], val);
+        }
         if constexpr (BOOK != kAffine) val *= rs_n;
-        float *dst = a.y + (size_t)m * a.y_stride + n;
-        *dst = ACC ? *dst + val : val;
+        float *dst = yout + (size_t)m * ystride + n;
+        *dst = acc_here ? *dst + val : val;
       }
     }
   }
@@ -367,12 +379,28 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
 
 // ------------------------------------------------------------------ host
 
-size_t gemm4_workspace(int book, int M, int K) {
+// K is split in two when the reduction is long against the output width (K >= 2N, and
+// at least 32 group pairs): the down projections, whose few output tiles would otherwise
+// leave most of the chip idle in the last round of workgroups. The choice depends on the
+// shape only, never on M, so a token's result is the same whatever the batch.
+static bool split_k(int K, int N) { return K >= 2 * N && (K / kGroup + 1) / 2 >= 32; }
+
+static size_t books_workspace(int book, int M, int K) {
   const int G = K / kGroup;
   const size_t gs_stride = (size_t)(2 * G + 31) / 32 * 32;
-  if (book == kAffine) return ((size_t)M * K * 2 + 255) / 256 * 256 + (size_t)M * gs_stride * 2;
-  if (book == kInt16) return (size_t)(G + 1) * ((M + 127) / 128 * 128) * sizeof(float);
+  if (book == kAffine) return ((size_t)M * K * 2 + 255) / 256 * 256 + ((size_t)M * gs_stride * 2 + 255) / 256 * 256;
+  if (book == kInt16) return ((size_t)(G + 1) * ((M + 127) / 128 * 128) * sizeof(float) + 255) / 256 * 256;
   return 0;
+}
+
+size_t gemm4_workspace(int book, int M, int K, int N) {
+  return books_workspace(book, M, K) + (split_k(K, N) ? (size_t)M * N * sizeof(float) : 0);
+}
+
+// y[m][n] += part[m][n]: the second half of a split K, added in a fixed order.
+__global__ void split_add_kernel(float *y, int y_stride, const float *part, int part_stride, int M, int N) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
+  if (n < N && m < M) y[(size_t)m * y_stride + n] += part[(size_t)m * part_stride + n];
 }
 
 template <int BOOK, int SD>
@@ -391,7 +419,7 @@ static int launch_gemm4_inst(int accum, dim3 grid, size_t lds, hipStream_t st, c
 int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
               const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st) {
   const int G = K / kGroup;
-  const size_t need = gemm4_workspace(book, M, K);
+  const size_t need = gemm4_workspace(book, M, K, N);
   RLQ_REQUIRE(ws_bytes >= need, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
   RLQ_REQUIRE(need == 0 || aligned(ws, 256), "workspace must be 256-byte aligned");
   RLQ_REQUIRE((size_t)M * std::max(x_stride, K) * 2 < (1ull << 31), "prefill kernel: x spans more than 2 GiB");
@@ -420,8 +448,14 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
       a.asum = asum;
     }
   }
+  const bool split = split_k(K, N);
+  a.np_first = split ? (G + 1) / 2 / 2 : (G + 1) / 2;
+  if (split) {
+    a.y_part = reinterpret_cast<float *>(static_cast<char *>(ws) + books_workspace(book, M, K));
+    a.y_part_stride = N;
+  }
   const int mblocks = (M + kGM - 1) / kGM, nblocks = (N + kGN - 1) / kGN;
-  const dim3 grid(mblocks * nblocks);
+  const dim3 grid(mblocks * nblocks, split ? 2 : 1);
   const size_t lds = (size_t)kStages * kStageBytes;
   int rc;
   switch (book) {
@@ -434,6 +468,10 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
   }
   if (rc) return rc;
   RLQ_HIP(hipGetLastError());
+  if (split) {
+    split_add_kernel<<<dim3((N + 255) / 256, M), 256, 0, st>>>(y, y_stride, a.y_part, a.y_part_stride, M, N);
+    RLQ_HIP(hipGetLastError());
+  }
   return 0;
 }
 

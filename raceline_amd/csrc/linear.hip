@@ -530,8 +530,8 @@ int rlq_linear_native(const void *x, int x_stride, int M, int K, int N, const vo
 size_t rlq_linear_workspace_bytes(int M, int K, int N) {
   if (M <= 0 || K <= 0 || N <= 0 || K % kGroup) return 0;
   // the largest of the books (the affine prefill kernel's prepped activations)
-  return std::max({M <= kGemvMaxM ? gemv_workspace(M, K, N) : (size_t)0, gemm4_workspace(kAffine, M, K),
-                   gemm4_workspace(kInt16, M, K)});
+  return std::max({M <= kGemvMaxM ? gemv_workspace(M, K, N) : (size_t)0, gemm4_workspace(kAffine, M, K, N),
+                   gemm4_workspace(kInt16, M, K, N), gemm4_workspace(kInt15, M, K, N)});
 }
 
 int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int K, int N, const void *packed,

@@ -86,7 +86,9 @@ def test_gemv_accumulates(gpu, M, K, N):
 GEMM_CASES = [(9, 512, 96), (16, 1024, 300), (32, 2048, 1024), (33, 256, 64), (130, 5120, 1024),
               (512, 2048, 1024), (70, 9216, 2560), (256, 1024, 300), (40, 2560, 1000),
               # an odd number of groups (the last pair half empty), a single group, ragged M and N
-              (129, 320, 17), (64, 64, 48), (200, 576, 272), (300, 192, 513)]
+              (129, 320, 17), (64, 64, 48), (200, 576, 272), (300, 192, 513),
+              # K split in two halves (K >= 2N, >= 32 group pairs), with an odd number of groups
+              (100, 4160, 1000)]
 
 
 @pytest.mark.parametrize("M,K,N", GEMM_CASES)
@@ -99,8 +101,8 @@ def test_gemm_parity(gpu, M, K, N):
     O.check_close(y, ref, TOL, f"gemm M={M} K={K} N={N}")
 
 
-def test_gemm_accumulates(gpu):
-    M, K, N = 200, 1024, 384
+@pytest.mark.parametrize("M,K,N", [(200, 1024, 384), (150, 8192, 1024)])   # the second splits K
+def test_gemm_accumulates(gpu, M, K, N):
     q, s, b = make_layer(1, N, K)
     x = make_x(2, M, K)
     y0 = np.random.default_rng(3).standard_normal((M, N)).astype(np.float32)
@@ -121,10 +123,12 @@ def test_rows_do_not_depend_on_other_rows(gpu):
         np.testing.assert_array_equal(y_one[0], y_all[m])
 
 
-def test_gemm_rows_do_not_depend_on_other_rows(gpu):
+@pytest.mark.parametrize("K,N", [(2048, 640), (8192, 1024)])   # the second splits K
+def test_gemm_rows_do_not_depend_on_other_rows(gpu, K, N):
     """The prefill kernel keeps the same rule: rows 50..119 alone (M = 70) give the same
-    bits as inside M = 200, wherever the 128-row tiles fall."""
-    M, K, N = 200, 2048, 640
+    bits as inside M = 200, wherever the 128-row tiles fall (the split of K depends on the
+    shape of the weight only)."""
+    M = 200
     q, s, b = make_layer(15, N, K)
     x = make_x(16, M, K)
     wt = upload(q, s, b, "f16", gpu)

@@ -75,7 +75,7 @@ def test_native_parity(gpu, book, M, K, N):
 @pytest.mark.parametrize("book", BOOKS)
 def test_native_accumulates(gpu, book):
     rng = np.random.default_rng(77)
-    for M, K, N in ((2, 1024, 256), (40, 1024, 256)):
+    for M, K, N in ((2, 1024, 256), (40, 1024, 256), (40, 8192, 512)):   # the last splits K
         q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
         s_row = rng.uniform(0.002, 0.02, size=N).astype(np.float32)
         x = rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)

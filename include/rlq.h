@@ -80,9 +80,11 @@ int rlq_repack_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const uint16
 
 /* ---------------------------------------------------------------- dense affine linear */
 
-/* Bytes of scratch rlq_linear_affine needs for these sizes (0 for the decode kernel; the
- * prefill kernel stages the activations' group sums there). Contents need no initialisation
- * and are not kept between calls; calls that share one workspace must not overlap. */
+/* Bytes of scratch rlq_linear_affine and rlq_linear_native need for these sizes (0 for the
+ * decode kernel; the prefill kernel stages the prepared activations and their group sums
+ * there, and, for a weight whose K it splits in two (K >= 2N), the second half's partial
+ * products). Contents need no initialisation and are not kept between calls; calls that
+ * share one workspace must not overlap. */
 size_t rlq_linear_workspace_bytes(int M, int K, int N);
 
 /* y[m][n] = sum_k x[m][k] * W[n][k]   (accum = 0)
@@ -123,7 +125,8 @@ int rlq_pack_native_blocked(const uint8_t *w_blk, int K, int n_pad, int row0, in
 /* y[m][n] (+)= s_row[n] * sum_k x[m][k] * L[q[n][k]]  (+ 0.5 * sum_k x[m][k] inside the row
  * scale for RLQ_BOOK_INT16). Replaces linear_q4n (kernels/linear.metal:118-184). x fp16
  * [M][x_stride] (column scale already applied); s_row fp32 [N]; y fp32 [M][y_stride]. The
- * workspace (rlq_linear_workspace_bytes) is used by M > 8 with RLQ_BOOK_INT16 only. */
+ * workspace (rlq_linear_workspace_bytes) is used for M > 8 by RLQ_BOOK_INT16 and by weights
+ * whose K the prefill kernel splits. */
 int rlq_linear_native(const void *x, int x_stride, int M, int K, int N, const void *packed, const float *s_row,
                       int book, float *y, int y_stride, int accum, void *workspace, size_t workspace_bytes,
                       void *stream);

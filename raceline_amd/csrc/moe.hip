@@ -278,13 +278,17 @@ __global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
 // The same products with the item's token rows staged once per workgroup: a workgroup
 // takes one work item and `tiles_per_block` consecutive 16-row weight tiles of its expert,
 // each split over K between `waves_per_tile` waves (wave = tile * waves_per_tile + part).
-// The item's 16 rows are read first (through the row -> token map for gate/up), then every
-// weight load of the workgroup is issued, and the rows go to LDS in operand order while
-// the weights are in flight; every tile of the workgroup then reads them from LDS. (The
-// per-tile kernel above reads each row once per tile and wave from L2.) LDS: 16 rows of
-// K + 8 halves (the pad keeps the 16 rows of an operand read in distinct banks), then the
-// partials of parts 1.. of every tile. XPT: activation chunks (8 halves) per thread.
-template <int GPW, int SD, int KIND, int XPT>
+// Wave w stages rows w, w + waves, ... of the item (one token index per row, a uniform
+// load through the row -> token map for gate/up): its first row's loads are issued, then
+// every weight load of the wave, and the row goes to LDS in operand order while the
+// weights are in flight. The group sums of the 16 rows are then formed once for all the
+// workgroup's tiles (group_sums), and every tile reads rows and sums from LDS. (The
+// per-tile kernel above reads each row once per tile and wave from L2 and forms the sums
+// per tile: the same products, so the two kernels give the same bits.) LDS: 16 rows of
+// K + 8 halves (the pad keeps the 16 rows of an operand read in distinct banks), the
+// group sums [G][16] floats, then the partials of parts 1.. of every tile. CPL: chunks of
+// 8 halves per lane and row (K / 512, rounded up).
+template <int GPW, int SD, int KIND, int CPL>
 __global__ __launch_bounds__(1024) void moe_expert_lds_kernel(MoeArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int item = blockIdx.y;
@@ -305,41 +309,57 @@ __global__ __launch_bounds__(1024) void moe_expert_lds_kernel(MoeArgs a) {
   const int wn = tile_ok ? max(0, min(G, wg0 + GPW) - wg0) : 0;
   const int rstride = a.K + 8;
   _Float16 *xs = reinterpret_cast<_Float16 *>(lds);
-  f32x4 *red = reinterpret_cast<f32x4 *>(lds + (size_t)16 * rstride * 2);
+  float *gsl = reinterpret_cast<float *>(lds + (size_t)16 * rstride * 2);
+  f32x4 *red = reinterpret_cast<f32x4 *>(gsl + (size_t)G * 16);
+  const int nw = nthreads >> 6, cpr = a.K / 8;
 
-  // 1. the item's rows (chunk c of row r: 8 halves), rows >= rows read zeros
-  const int cpr = a.K / 8;
+  // 1. the wave's first row (lane l: chunks l, l + 64, ... of 8 halves); rows past the
+  // item's read zeros
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)((size_t)a.x_rows * a.x_stride * 2));
-  u32x4 xr[XPT];
+  auto load_row = [&](int row, u32x4 (&xr)[CPL]) {
+    const bool ok = row < rows;
+    const int src = KIND == 0 ? a.tok[r0 + (ok ? row : 0)] : r0 + row;
 #pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    const int chunk = tid + i * nthreads;
-    const int r = chunk / cpr, c = chunk - r * cpr;
-    uint32_t off = kFarOffset;
-    if (chunk < 16 * cpr && r < rows) {
-      const int src = KIND == 0 ? a.tok[r0 + r] : r0 + r;
-      off = (uint32_t)(((size_t)src * a.x_stride + 8 * c) * 2);
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      const uint32_t off = ok && c < cpr ? (uint32_t)(((size_t)src * a.x_stride + 8 * c) * 2) : kFarOffset;
+      xr[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
     }
-    xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
-  }
+  };
+  auto store_row = [&](int row, const u32x4 (&xr)[CPL]) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      if (c < cpr) *reinterpret_cast<u32x4 *>(xs + (size_t)row * rstride + 8 * c) = prep_x8(xr[j]);
+    }
+  };
+  u32x4 xr[CPL];
+  load_row(wave, xr);
   // 2. every weight load of this wave's part of its tile
   u32x4 wq[GPW / 2], sq[GPW / 4];
   const WaveTile wt = wave_tile(a.codes, a.sb, t, G4, wg0, wn > 0 ? GPW : 0);
   issue_tile_loads<GPW>(wt, lane, wq, sq);
   __builtin_amdgcn_sched_barrier(0);
-  // 3. rows -> LDS in operand order (the loads complete in issue order: this waits for the
-  // rows only)
-#pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    const int chunk = tid + i * nthreads;
-    if (chunk < 16 * cpr) {
-      const int r = chunk / cpr, c = chunk - r * cpr;
-      *reinterpret_cast<u32x4 *>(xs + (size_t)r * rstride + 8 * c) = prep_x8(xr[i]);
-    }
+  // 3. rows -> LDS in operand order (loads complete in issue order: the first row waits
+  // for its own loads only); a workgroup of fewer than 16 waves stages the rest in turn
+  store_row(wave, xr);
+  for (int row = wave + nw; row < 16; row += nw) {
+    load_row(row, xr);
+    store_row(row, xr);
   }
   __syncthreads();
-  // 4. products, then the parts of each tile meet in part order
-  f32x4 acc = tile_dot_lds<GPW, SD>(wq, sq, xs + (size_t)wg0 * kGroup, rstride, wn, lane);
+  // 4. the group sums of the 16 rows, once for every tile: wave w forms groups w, w + nw, ...
+  for (int g = wave; g < G; g += nw) {
+    const _Float16 *xa = xs + (size_t)c16 * rstride + 8 * j4 + (size_t)g * kGroup;
+    half8 af[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(xa + 32 * s);
+    const f32x4 gsv = group_sums(af);
+    if (c16 == 0) *reinterpret_cast<f32x4 *>(gsl + (size_t)g * 16 + 4 * j4) = gsv;
+  }
+  __syncthreads();
+  // 5. products, then the parts of each tile meet in part order
+  f32x4 acc = tile_dot_lds<GPW, SD>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn, lane);
   if (part > 0) red[((size_t)tt * (W - 1) + part - 1) * 64 + lane] = acc;
   __syncthreads();
   if (part != 0 || !tile_ok) return;
@@ -405,16 +425,26 @@ constexpr int kStagedMaxK = 4096;
 constexpr int kStagedMinTokens = 8;
 static int staged_gpw(int K) { return K <= 1024 ? 8 : 16; }
 
+// Waves per workgroup. Two workgroups per CU let one stream weights while the other stages
+// rows or multiplies. With 16 groups per wave the kernel holds 80 VGPRs (6 waves per SIMD,
+// 24 per CU), so where LDS leaves room for two workgroups they take 12 waves each; with 8
+// groups per wave (about 52 VGPRs) two workgroups of 16 waves fit. Measured on the MoE
+// layer at T = 512 (H = 2048, I = 512): gate/up 206 -> 184 us per layer going from 16 to
+// 12 waves; 8 and 16 waves for down within 2 us.
+static int staged_waves(int gpw, size_t lds_bytes) {
+  return gpw == 16 && 2 * lds_bytes <= kMaxLdsBytes ? 12 : 16;
+}
+
 template <int GPW, int SD, int KIND>
 static int launch_staged_inst(int tpe, hipStream_t st, MoeArgs a, int items) {
   const int G = a.K / kGroup, W = (G + GPW - 1) / GPW;
-  const int tpb = std::max(1, std::min(tpe, 16 / W));
+  const size_t lds_rows = (size_t)16 * (a.K + 8) * 2 + (size_t)G * 16 * 4;
+  const int tpb = std::max(1, std::min(tpe, staged_waves(GPW, lds_rows + (size_t)(16 / W) * (W - 1) * 1024) / W));
   a.tiles_per_block = tpb;
   a.waves_per_tile = W;
   const int threads = 64 * W * tpb;
-  const int chunks = 16 * (a.K / 8);
-  const int xpt = (chunks + threads - 1) / threads;
-  const size_t lds = (size_t)16 * (a.K + 8) * 2 + (size_t)tpb * (W - 1) * 64 * 16;
+  const int xpt = (a.K / 8 + 63) / 64;   // chunks of 8 halves per lane and row
+  const size_t lds = lds_rows + (size_t)tpb * (W - 1) * 64 * 16;
   const dim3 grid((tpe + tpb - 1) / tpb, items);
   static LdsOptIn lds_opt[4];
   const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1>),

@@ -157,22 +157,40 @@ __device__ __forceinline__ void native_step(f32x4 &acc, f32x4 &asum, const half8
 }
 
 
+// The activation sums of one group for 16 token rows, as two products with a constant
+// operand (lane (c16, j4) gets rows 4 j4 + v; the 16 of the odd positions undoes the 1/16
+// that prep_x8 puts on the odd codes' activations). Every tile of the same rows needs the
+// same sums: a caller that forms them once and hands them to group_step_gs gets the bits
+// group_step gets.
+__device__ __forceinline__ f32x4 group_sums(const half8 (&af)[2]) {
+  const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x4C004C00u, 0x3C003C00u, 0x4C004C00u});  // 1, 16
+  f32x4 gsv = {};
+#pragma unroll
+  for (int s = 0; s < 2; ++s) gsv = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, gsv, 0, 0, 0);
+  return gsv;
+}
+
+// One group jg of the wave's part with the group's activation sums given: acc[r] +=
+// s * (x . q) + b * gsv[r] for the first NACC accumulator rows.
+template <int GPW, int SD, int NACC>
+__device__ __forceinline__ void group_step_gs(f32x4 &acc, const half8 (&af)[2], const f32x4 &gsv,
+                                              const u32x4 (&wq)[GPW / 2], const u32x4 (&sq)[GPW / 4], int jg) {
+  f32x4 p = {};
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], nib8_to_half8_oddx16(wq[jg >> 1][2 * (jg & 1) + s]), p, 0, 0, 0);
+  const uint32_t pr = sq[jg >> 2][jg & 3];
+  const float sc = fma_scale<SD, 0>(pr, kTwo24, 0.0f);   // s * 2^24, exact: undoes the codes' 2^-24
+#pragma unroll
+  for (int r = 0; r < NACC; ++r) acc[r] = fma_scale<SD, 1>(pr, gsv[r], __builtin_fmaf(sc, p[r], acc[r]));
+}
+
 // One group jg of the wave's part: acc[r] += s * (x . q) + b * gsum for the first NACC
 // accumulator rows (NACC = 1 when only token row 0 is live).
 template <int GPW, int SD, int NACC>
 __device__ __forceinline__ void group_step(f32x4 &acc, const half8 (&af)[2], const u32x4 (&wq)[GPW / 2],
                                            const u32x4 (&sq)[GPW / 4], int jg) {
-  const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x4C004C00u, 0x3C003C00u, 0x4C004C00u});  // 1, 16
-  f32x4 p = {}, gsv = {};
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], nib8_to_half8_oddx16(wq[jg >> 1][2 * (jg & 1) + s]), p, 0, 0, 0);
-    gsv = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, gsv, 0, 0, 0);
-  }
-  const uint32_t pr = sq[jg >> 2][jg & 3];
-  const float sc = fma_scale<SD, 0>(pr, kTwo24, 0.0f);   // s * 2^24, exact: undoes the codes' 2^-24
-#pragma unroll
-  for (int r = 0; r < NACC; ++r) acc[r] = fma_scale<SD, 1>(pr, gsv[r], __builtin_fmaf(sc, p[r], acc[r]));
+  group_step_gs<GPW, SD, NACC>(acc, af, group_sums(af), wq, sq, jg);
 }
 
 // The per-group step of any book: affine (group_step, scales applied per group) or native.
@@ -228,27 +246,27 @@ __device__ __forceinline__ f32x4 tile_dot_rows(const WaveTile &w, __amdgpu_buffe
   return acc;
 }
 
-// The wave's part of a 16-row weight tile (its loads already issued into wq, sq) times 16
-// token rows staged in LDS in operand order: xs points at row 0's element 64 * wg0 (the
-// wave's first group), rows rstride halves apart. Lane (c16, j4) reads row c16.
-template <int GPW, int SD, int BOOK = kAffine>
+// The wave's part of a 16-row affine weight tile (its loads already issued into wq, sq)
+// times 16 token rows staged in LDS in operand order, with their group sums formed
+// beforehand (group_sums): xs points at row 0's element 64 * wg0 (the wave's first group),
+// rows rstride halves apart; gs at the sums of group wg0, 16 floats (row order) per group.
+// Lane (c16, j4) reads row c16.
+template <int GPW, int SD>
 __device__ __forceinline__ f32x4 tile_dot_lds(const u32x4 (&wq)[GPW / 2], const u32x4 (&sq)[GPW / 4],
-                                              const _Float16 *xs, int rstride, int wn, int lane) {
+                                              const _Float16 *xs, const float *gs, int rstride, int wn, int lane) {
   const _Float16 *xa = xs + (lane & 15) * rstride + 8 * (lane >> 4);
-  f32x4 acc = {}, asum = {};
+  const float *ga = gs + 4 * (lane >> 4);
+  f32x4 acc = {};
 #pragma unroll
   for (int jg = 0; jg < GPW; ++jg) {
     if (jg < wn) {   // uniform: the groups past the wave's range add nothing
       half8 af[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(xa + jg * kGroup + 32 * s);
-      book_step<GPW, SD, 4, BOOK>(acc, asum, af, wq, sq, jg);
+      const f32x4 gsv = *reinterpret_cast<const f32x4 *>(ga + 16 * jg);
+      group_step_gs<GPW, SD, 4>(acc, af, gsv, wq, sq, jg);
       asm volatile("" : "+v"(acc));
     }
-  }
-  if constexpr (BOOK == kInt16) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(0.5f, asum[v], acc[v]);
   }
   return acc;
 }

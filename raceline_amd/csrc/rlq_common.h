@@ -34,7 +34,9 @@ int check_hip(hipError_t e, const char *what);
 
 inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Lets a kernel use up to 160 KB of dynamic LDS on the current device. A function
+constexpr size_t kMaxLdsBytes = 160 * 1024;   // LDS of one gfx950 CU
+
+// Lets a kernel use up to kMaxLdsBytes of dynamic LDS on the current device. A function
 // attribute belongs to one device, so every device is set once; `done` is the call site's
 // record of the devices already set (bit d: device d; devices past 63 are set every call).
 struct LdsOptIn {

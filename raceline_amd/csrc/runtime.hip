@@ -37,7 +37,7 @@ int allow_large_lds(const void *fn, LdsOptIn &done) {
   RLQ_HIP(hipGetDevice(&dev));
   const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
   if (bit && (done.done.load(std::memory_order_acquire) & bit)) return 0;
-  RLQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  RLQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLdsBytes));
   if (bit) done.done.fetch_or(bit, std::memory_order_acq_rel);
   return 0;
 }

@@ -42,10 +42,40 @@ static inline int moe_max_items(int T, int E, int topk) {
 
 // ------------------------------------------------------------------ routing: top-k
 
+// Wave-wide max and sum, every lane getting the result: rows of 16 lanes combine through
+// DPP lane swizzles (quad [1,0,3,2], quad [2,3,0,1], half-row mirror, row mirror), then the
+// four row results are read as scalars and combined in row order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_lane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
+}
+
 // One wave per token. Lane l holds logits l, l + 64, ...; repeated wave-wide argmax with
 // ties to the lower expert (kernels/moe.metal:75-91). Weights: exp(l - max) over the
 // softmax denominator of all E logits, or over the chosen ones when norm_topk
 // (moe.metal:92-102); the shared slot gets sigmoid(logit[E]) (moe.metal:103-104).
+// A round takes the wave max of the lanes' best untaken logits, then the lowest expert
+// holding it: the first slot j whose ballot (logit == max, untaken) is not empty, and its
+// lowest lane. Every value of a round is wave-uniform; lane r keeps round r's pick.
 template <int EPL>
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int stride, int T, int E, int topk,
                                                        int norm_topk, int *sel, float *w) {
@@ -55,61 +85,51 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int 
   const int S = topk + 1;
   const float *row = logits + (size_t)t * stride;
   float v[EPL];
-  float m = -INFINITY;
+  float lm = -INFINITY;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
     const float l = e < E ? row[e] : -INFINITY;
     v[j] = l == l ? l : -INFINITY;            // a NaN logit ranks last
-    m = fmaxf(m, v[j]);
+    lm = fmaxf(lm, v[j]);
   }
-  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  float z = 0.0f;
+  const float m = wave_max(lm);
+  float lz = 0.0f;
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) z += (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
-  for (int o = 32; o >= 1; o >>= 1) z += __shfl_xor(z, o);
+  for (int j = 0; j < EPL; ++j) lz += (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
+  const float z = wave_sum(lz);
 
   // Chosen experts are tracked in `taken`, so every pick is a distinct expert < E even
   // when logits tie at -inf (topk <= E guarantees a candidate).
-  float top[kMaxTopk];
-  int which[kMaxTopk];
   uint32_t taken = 0;
+  int my_which = 0;
+  float my_ex = 0.0f, sum = 0.0f;
   for (int r = 0; r < topk; ++r) {
     float bv = -INFINITY;
-    int be = 1 << 30;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E && !((taken >> j) & 1u) && (v[j] > bv || (v[j] == bv && e < be))) {
-        bv = v[j];
-        be = e;
-      }
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oe = __shfl_xor(be, o);
-      if (ov > bv || (ov == bv && oe < be)) {
-        bv = ov;
-        be = oe;
-      }
-    }
-    top[r] = bv;
-    which[r] = be;
 #pragma unroll
     for (int j = 0; j < EPL; ++j)
-      if (lane + 64 * j == be) taken |= 1u << j;
+      if (lane + 64 * j < E && !((taken >> j) & 1u)) bv = fmaxf(bv, v[j]);
+    const float top = wave_max(bv);
+    int be = -1;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const uint64_t b = __ballot(lane + 64 * j < E && !((taken >> j) & 1u) && v[j] == top);
+      if (be < 0 && b != 0) be = 64 * j + __builtin_ctzll(b);
+    }
+    if (be >= 0 && lane == (be & 63)) taken |= 1u << (be >> 6);
+    const float ex = expf(top - m);
+    sum += ex;
+    if (lane == r) {
+      my_which = be;
+      my_ex = ex;
+    }
+  }
+  const float denom = norm_topk ? sum : z;
+  if (lane < topk) {
+    sel[t * S + lane] = my_which;
+    w[t * S + lane] = my_ex / denom;
   }
   if (lane == 0) {
-    float ex[kMaxTopk], sum = 0.0f;
-    for (int r = 0; r < topk; ++r) {
-      ex[r] = expf(top[r] - m);
-      sum += ex[r];
-    }
-    const float denom = norm_topk ? sum : z;
-    for (int r = 0; r < topk; ++r) {
-      sel[t * S + r] = which[r];
-      w[t * S + r] = ex[r] / denom;
-    }
     sel[t * S + topk] = E;
     w[t * S + topk] = 1.0f / (1.0f + expf(-row[E]));
   }

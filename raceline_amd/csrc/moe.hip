@@ -32,6 +32,7 @@ namespace rlq {
 constexpr int kItemRows = 16;     // rows per work item: the MFMA tile height
 constexpr int kMaxTopk = 16;
 constexpr int kMaxExperts = 1023; // E; E + 1 <= 1024 (one thread per expert in the sort)
+constexpr int kRouteSmallTokens = 16;   // up to this many tokens route in one launch (a wave each)
 
 // Most work items a call can have: sum over experts of ceil(rows_e / 16) <= A / 16 + the
 // number of experts with rows, which is at most min(E + 1, A).
@@ -77,13 +78,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // holding it: the first slot j whose ballot (logit == max, untaken) is not empty, and its
 // lowest lane. Every value of a round is wave-uniform; lane r keeps round r's pick.
 template <int EPL>
-__global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int stride, int T, int E, int topk,
-                                                       int norm_topk, int *sel, float *w) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const int S = topk + 1;
-  const float *row = logits + (size_t)t * stride;
+__device__ void topk_token(const float *row, int E, int topk, int norm_topk, int *sel_t, float *w_t, int lane) {
   float v[EPL];
   float lm = -INFINITY;
 #pragma unroll
@@ -126,13 +121,22 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int 
   }
   const float denom = norm_topk ? sum : z;
   if (lane < topk) {
-    sel[t * S + lane] = my_which;
-    w[t * S + lane] = my_ex / denom;
+    sel_t[lane] = my_which;
+    w_t[lane] = my_ex / denom;
   }
   if (lane == 0) {
-    sel[t * S + topk] = E;
-    w[t * S + topk] = 1.0f / (1.0f + expf(-row[E]));
+    sel_t[topk] = E;
+    w_t[topk] = 1.0f / (1.0f + expf(-row[E]));
   }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int stride, int T, int E, int topk,
+                                                       int norm_topk, int *sel, float *w) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const size_t a0 = (size_t)t * (topk + 1);
+  topk_token<EPL>(logits + (size_t)t * stride, E, topk, norm_topk, sel + a0, w + a0, threadIdx.x & 63);
 }
 
 // ------------------------------------------------------------------ routing: sort
@@ -167,9 +171,8 @@ __device__ int block_exclusive_scan(int v, int *wave_tot, int *total) {
 // token t's row for expert e is off[e] + (tokens before t that chose e), counted with one
 // bitmap per expert over a chunk of tokens and prefix popcounts (a token chooses an expert
 // at most once). LDS: counts and offsets, then per chunk bm[E+1][wpe] and pre[E+1][wpe].
-__global__ __launch_bounds__(1024) void moe_sort_kernel(const int *sel, int T, int E, int S, int wpe, int *tok,
-                                                        int *inv, int4 *items, int *n_items) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+__device__ void sort_assignments(const int *sel, int T, int E, int S, int wpe, int *tok, int *inv, int4 *items,
+                                 int *n_items, unsigned char *lds) {
   int *cnt = reinterpret_cast<int *>(lds);      // [1024]
   int *off = cnt + 1024;                        // [1024]
   int *run = off + 1024;                        // [1024]
@@ -229,6 +232,28 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int *sel, int T, i
     if (tid < E1) run[tid] += (int)(pre[(size_t)tid * wpe + wpe - 1] + __popc(bm[(size_t)tid * wpe + wpe - 1]));
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(1024) void moe_sort_kernel(const int *sel, int T, int E, int S, int wpe, int *tok,
+                                                        int *inv, int4 *items, int *n_items) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  sort_assignments(sel, T, E, S, wpe, tok, inv, items, n_items, lds);
+}
+
+// Routing of up to 16 tokens in one launch: wave t picks token t's experts, then the whole
+// workgroup sorts (the same steps as moe_topk_kernel followed by moe_sort_kernel; sel and w
+// are written to memory and read back after the barrier, which makes them visible to the
+// workgroup).
+template <int EPL>
+__global__ __launch_bounds__(1024) void moe_route_small_kernel(const float *logits, int stride, int T, int E, int topk,
+                                                               int norm_topk, int wpe, int *sel, float *w, int *tok,
+                                                               int *inv, int4 *items, int *n_items) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int t = threadIdx.x >> 6;
+  const size_t a0 = (size_t)t * (topk + 1);
+  if (t < T) topk_token<EPL>(logits + (size_t)t * stride, E, topk, norm_topk, sel + a0, w + a0, threadIdx.x & 63);
+  __syncthreads();
+  sort_assignments(sel, T, E, topk + 1, wpe, tok, inv, items, n_items, lds);
 }
 
 // ------------------------------------------------------------------ grouped expert matmuls
@@ -410,17 +435,27 @@ __global__ __launch_bounds__(1024) void moe_expert_lds_kernel(MoeArgs a) {
 // ------------------------------------------------------------------ combine
 
 // h[t][d] += sum over slots s of w[t*S + s] * y[inv[t*S + s]][d], the slots in order
-// (moe.metal:157-174).
+// (moe.metal:157-174). A thread takes V consecutive d (V = 4 when rows and pointers allow
+// 16-byte accesses); every component follows the same order of fused multiply-adds.
+template <int V>
 __global__ void moe_combine_kernel(const float *y, int y_stride, const int *inv, const float *w, int T, int S, int H,
                                    float *h, int h_stride) {
-  const int d = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  typedef float fvec __attribute__((ext_vector_type(V)));
+  const int d = (blockIdx.x * blockDim.x + threadIdx.x) * V, t = blockIdx.y;
   if (d >= H || t >= T) return;
-  float acc = 0.0f;
+  fvec acc = {};
   for (int s = 0; s < S; ++s) {
     const int a = t * S + s;
-    acc += w[a] * y[(size_t)inv[a] * y_stride + d];
+    const float ws = w[a];
+    const fvec yv = *reinterpret_cast<const fvec *>(y + (size_t)inv[a] * y_stride + d);
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = __builtin_fmaf(ws, yv[v], acc[v]);
   }
-  h[(size_t)t * h_stride + d] += acc;
+  fvec *hp = reinterpret_cast<fvec *>(h + (size_t)t * h_stride + d);
+  fvec hv = *hp;
+#pragma unroll
+  for (int v = 0; v < V; ++v) hv[v] += acc[v];
+  *hp = hv;
 }
 
 // ------------------------------------------------------------------ host side
@@ -531,16 +566,39 @@ int rlq_moe_route(const float *logits, int logit_stride, int T, int E, int topk,
   RLQ_REQUIRE(logits && sel && w && tok && inv && items && n_items, "rlq_moe_route: null pointer argument");
   RLQ_REQUIRE(aligned(items, 16), "rlq_moe_route: items must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 g1((T + 3) / 4);
   const int epl = (E + 63) / 64;
+  const int wpe = sort_wpe(E);
+  const size_t lds = sort_lds_bytes(E, wpe);
+  if (T <= kRouteSmallTokens) {
+    // one launch: the top-k of each token by its own wave, then the sort
+    static LdsOptIn small_opt[5];
+    const int which = epl <= 1 ? 0 : epl <= 2 ? 1 : epl <= 4 ? 2 : epl <= 8 ? 3 : 4;
+    const void *fns[5] = {reinterpret_cast<const void *>(&moe_route_small_kernel<1>),
+                          reinterpret_cast<const void *>(&moe_route_small_kernel<2>),
+                          reinterpret_cast<const void *>(&moe_route_small_kernel<4>),
+                          reinterpret_cast<const void *>(&moe_route_small_kernel<8>),
+                          reinterpret_cast<const void *>(&moe_route_small_kernel<16>)};
+    if (int rc = allow_large_lds(fns[which], small_opt[which])) return rc;
+    int4 *it4 = reinterpret_cast<int4 *>(items);
+#define RLQ_ROUTE_SMALL(N)                                                                                             \
+  moe_route_small_kernel<N><<<1, 1024, lds, st>>>(logits, logit_stride, T, E, topk, norm_topk, wpe, sel, w, tok, inv, \
+                                                  it4, n_items)
+    if (epl <= 1) RLQ_ROUTE_SMALL(1);
+    else if (epl <= 2) RLQ_ROUTE_SMALL(2);
+    else if (epl <= 4) RLQ_ROUTE_SMALL(4);
+    else if (epl <= 8) RLQ_ROUTE_SMALL(8);
+    else RLQ_ROUTE_SMALL(16);
+#undef RLQ_ROUTE_SMALL
+    RLQ_HIP(hipGetLastError());
+    return 0;
+  }
+  const dim3 g1((T + 3) / 4);
   if (epl <= 1) moe_topk_kernel<1><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
   else if (epl <= 2) moe_topk_kernel<2><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
   else if (epl <= 4) moe_topk_kernel<4><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
   else if (epl <= 8) moe_topk_kernel<8><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
   else moe_topk_kernel<16><<<g1, 256, 0, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w);
   RLQ_HIP(hipGetLastError());
-  const int wpe = sort_wpe(E);
-  const size_t lds = sort_lds_bytes(E, wpe);
   static LdsOptIn lds_opt;
   if (int rc = allow_large_lds(reinterpret_cast<const void *>(&moe_sort_kernel), lds_opt)) return rc;
   moe_sort_kernel<<<1, 1024, lds, st>>>(sel, T, E, topk + 1, wpe, tok, inv, reinterpret_cast<int4 *>(items), n_items);
@@ -611,9 +669,11 @@ int rlq_moe_combine(const float *y, int y_stride, const int *inv, const float *w
   RLQ_REQUIRE(T >= 1 && H >= 1 && topk >= 1 && topk <= kMaxTopk, "rlq_moe_combine: T=%d H=%d topk=%d", T, H, topk);
   RLQ_REQUIRE(y && inv && w && h, "rlq_moe_combine: null pointer argument");
   RLQ_REQUIRE(y_stride >= H && h_stride >= H, "rlq_moe_combine: strides must be >= H");
-  const dim3 grid((H + 255) / 256, T);
-  moe_combine_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(y, y_stride, inv, w, T, topk + 1, H, h,
-                                                                         h_stride);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (H % 4 == 0 && y_stride % 4 == 0 && h_stride % 4 == 0 && aligned(y, 16) && aligned(h, 16))
+    moe_combine_kernel<4><<<dim3((H + 1023) / 1024, T), 256, 0, st>>>(y, y_stride, inv, w, T, topk + 1, H, h, h_stride);
+  else
+    moe_combine_kernel<1><<<dim3((H + 255) / 256, T), 256, 0, st>>>(y, y_stride, inv, w, T, topk + 1, H, h, h_stride);
   RLQ_HIP(hipGetLastError());
   return 0;
 }

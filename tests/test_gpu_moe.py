@@ -57,7 +57,8 @@ def _sync():
 
 
 @pytest.mark.parametrize("T,E,topk,norm", [(1, 16, 4, True), (7, 16, 4, False), (40, 64, 8, True),
-                                           (300, 256, 8, True), (1, 256, 8, True), (2000, 8, 2, True)])
+                                           (300, 256, 8, True), (1, 256, 8, True), (2000, 8, 2, True),
+                                           (16, 256, 8, True), (17, 64, 8, False), (16, 700, 16, False)])
 def test_route(gpu, T, E, topk, norm):
     from raceline_amd import ops
 
@@ -203,3 +204,33 @@ def test_token_result_same_across_kernel_choice(gpu):
     assert torch.equal(h5, h[3:8])
     ref, _, _ = O.moe_layer_f64(x[3:8], logits[3:8], gu, dn, E, topk, I, H)
     O.check_close(h5.cpu().numpy().astype(np.float64), ref, TOL, "moe per-tile vs staged")
+
+
+def test_combine_one_and_four_wide_paths_agree(gpu):
+    """The combine takes four floats per thread when rows and pointers allow 16-byte accesses
+    and one otherwise; both follow the same per-element order, so they give the same bits,
+    and both match h + sum_s w_s y_s in float64."""
+    import torch
+
+    from raceline_amd import ops
+
+    T, E, topk, H = 37, 16, 4, 192
+    S = topk + 1
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((T, E + 1), dtype=np.float32)
+    r = ops.moe_route(to_dev(logits, gpu), E, topk)
+    y = rng.standard_normal((T * S, H + 1)).astype(np.float32)
+    h0 = rng.standard_normal((T, H)).astype(np.float32)
+    y_odd = to_dev(y, gpu)[:, :H]                      # row stride H + 1: one float per thread
+    y_even = to_dev(np.ascontiguousarray(y[:, :H]), gpu)
+    h1, h4 = to_dev(h0, gpu), to_dev(h0, gpu)
+    ops.moe_combine(y_odd, r, h1)
+    ops.moe_combine(y_even, r, h4)
+    _sync()
+    assert torch.equal(h1, h4)
+    inv, w = r.inv.cpu().numpy(), r.w.cpu().numpy().astype(np.float64)
+    ref = h0.astype(np.float64).copy()
+    for t in range(T):
+        for s in range(S):
+            ref[t] += w[t * S + s] * y[inv[t * S + s], :H].astype(np.float64)
+    O.check_close(h4.cpu().numpy(), ref, TOL, "moe combine")

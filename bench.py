@@ -231,6 +231,28 @@ def bench_prefill(device, steps, warmup):
                                   "frac_of_mfma_peak": round(flops / tp / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}}
 
 
+def bench_decode(device, steps, warmup):
+    """BASELINE configs 2 and 3: the 9B layer (q/k/v stacked) at M = 1 and 5, the 27B layer at
+    M = 1 and 8, each step one pass over rotating weight copies."""
+    import torch
+
+    from raceline_amd.configs import CFG2_9B_STACKED, CFG3_27B
+
+    out = {}
+    for name, cfg, ms in (("9b", CFG2_9B_STACKED, (1, 5)), ("27b", CFG3_27B, (1, 8))):
+        layers = build_layer_copies(cfg, copies_for(cfg), 2, device, torch.float16)
+        for M in ms:
+            r = LayerRunner(layers, cfg, M, device)
+            t = time_steps(r, steps, warmup)
+            out[f"layer_{name}_m{M}"] = {"us_per_step": round(t * 1e6, 2),
+                                         "GB/s": round(layer_bytes(cfg, M) / t / 1e9, 1)}
+            log(f"[bench] {name} layer M={M}: {t * 1e6:.1f} us/step, {layer_bytes(cfg, M) / t / 1e9:.0f} GB/s")
+            del r
+        del layers
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_part(part, steps, warmup):
     import torch
 
@@ -239,7 +261,8 @@ def bench_part(part, steps, warmup):
     lib.load()
     dev = torch.device("cuda:0")
     log(f"[bench] part {part}")
-    return bench_prefill(dev, steps, warmup) if part == "prefill" else bench_moe(dev, steps, warmup)
+    fn = {"prefill": bench_prefill, "moe": bench_moe, "decode": bench_decode}[part]
+    return fn(dev, steps, warmup)
 
 
 def time_kernel(layers, shapes, M, idx, device, launches, kernel=0, outliers=0.0):
@@ -379,7 +402,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail configs, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--part", choices=["prefill", "moe"],
+    ap.add_argument("--part", choices=["prefill", "moe", "decode"],
                     help="run only this part of the detail (for rocprofv3); prints its figures as JSON")
     ap.add_argument("--profile", action="store_true",
                     help="launch only the dominant kernel and a calibration kernel (for rocprofv3)")

@@ -299,36 +299,106 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
   }
 }
 
+// Several tokens, two adjacent tiles per workgroup (t0 = 2 * block, t1 = t0 + 1): each wave
+// reads its activation operands once for both tiles (tile_dot_rows2). At M > 1 the
+// activations are a wave's largest stream (a group's operands are M * 128 bytes against
+// the 576 bytes of one tile's codes and scales, and they come from L2 once per tile), so
+// pairing halves it. Taken where a wave holds 8 groups: two tiles' loads then fit the
+// registers one tile of 16 groups takes. Each tile's sums are the one-tile kernel's, in
+// the same order, so the results do not depend on the pairing.
+template <int GPW, int SD, bool ACC, int BOOK>
+__global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int waves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, j4 = lane >> 4;
+  const int G = a.K / kGroup, G4 = quads_of(a.K);
+  const int tiles = tiles_of(a.N);
+  const int t0 = 2 * blockIdx.x, t1 = t0 + 1;
+  const int M = a.M;
+  f32x4 *red = reinterpret_cast<f32x4 *>(lds);   // [2][waves-1][64]
+
+  const int wg0 = wave * GPW;
+  const int wn = max(0, min(G, wg0 + GPW) - wg0);
+  const WaveTile w0 = wave_tile(a.codes, a.sb, t0, G4, wg0, GPW);
+  const WaveTile w1 = wave_tile(a.codes, a.sb, min(t1, tiles - 1), G4, wg0, t1 < tiles ? GPW : 0);
+  const uint32_t xrange = wn > 0 ? (uint32_t)((M - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
+  f32x4 acc0, acc1;
+  tile_dot_rows2<GPW, SD, BOOK>(w0, w1, rx, (uint32_t)c16 * a.x_stride * 2u + 16u * j4, c16 < M, wn, lane, acc0,
+                                acc1);
+
+  // the waves' partials meet in wave order, as in reduce_waves
+  if (wave > 0) {
+    red[(wave - 1) * 64 + lane] = acc0;
+    red[(waves - 1 + wave - 1) * 64 + lane] = acc1;
+  }
+  __syncthreads();
+  if (wave != 0 || 4 * j4 >= M) return;
+  for (int w = 1; w < waves; ++w) {
+    const f32x4 o0 = red[(w - 1) * 64 + lane], o1 = red[(waves - 1 + w - 1) * 64 + lane];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      acc0[v] += o0[v];
+      acc1[v] += o1[v];
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int n = 16 * (t0 + h) + c16;
+    if (n >= a.N) continue;
+    const float rs = BOOK == kAffine ? 1.0f : a.srow[n];
+    const f32x4 &acc = h ? acc1 : acc0;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * j4 + v;
+      if (m < M) {
+        float *dst = a.y + (size_t)m * a.y_stride + n;
+        const float val = BOOK == kAffine ? acc[v] : rs * acc[v];
+        *dst = ACC ? *dst + val : val;
+      }
+    }
+  }
+}
+
 static size_t gemv_workspace(int, int, int) { return 0; }
 
-template <int MAXM, int GPW, int SD, bool ACC, int BOOK>
+// PAIR: the two-tile kernel (M > 1 only).
+template <int MAXM, int GPW, int SD, bool ACC, int BOOK, bool PAIR>
 static int launch_gemv_inst(dim3 grid, int threads, size_t lds, hipStream_t st, const GemvArgs &a) {
   static LdsOptIn lds_opt;  // per instance and device, before its first launch there
-  if (int rc = allow_large_lds(reinterpret_cast<const void *>(&gemv_q4a_kernel<MAXM, GPW, SD, ACC, BOOK>), lds_opt))
-    return rc;
-  gemv_q4a_kernel<MAXM, GPW, SD, ACC, BOOK><<<grid, threads, lds, st>>>(a);
+  if constexpr (PAIR) {
+    if (int rc = allow_large_lds(reinterpret_cast<const void *>(&gemv_q4a_pair_kernel<GPW, SD, ACC, BOOK>), lds_opt))
+      return rc;
+    gemv_q4a_pair_kernel<GPW, SD, ACC, BOOK><<<grid, threads, lds, st>>>(a);
+  } else {
+    if (int rc = allow_large_lds(reinterpret_cast<const void *>(&gemv_q4a_kernel<MAXM, GPW, SD, ACC, BOOK>), lds_opt))
+      return rc;
+    gemv_q4a_kernel<MAXM, GPW, SD, ACC, BOOK><<<grid, threads, lds, st>>>(a);
+  }
   return 0;
 }
 
-template <int MAXM, int GPW, int BOOK>
+template <int MAXM, int GPW, int BOOK, bool PAIR>
 static int launch_gemv_acc(int sd, int accum, dim3 grid, int threads, size_t lds, hipStream_t st, const GemvArgs &a) {
   if constexpr (BOOK == kAffine) {
     if (sd == RLQ_BF16)
-      return accum ? launch_gemv_inst<MAXM, GPW, 1, true, BOOK>(grid, threads, lds, st, a)
-                   : launch_gemv_inst<MAXM, GPW, 1, false, BOOK>(grid, threads, lds, st, a);
+      return accum ? launch_gemv_inst<MAXM, GPW, 1, true, BOOK, PAIR>(grid, threads, lds, st, a)
+                   : launch_gemv_inst<MAXM, GPW, 1, false, BOOK, PAIR>(grid, threads, lds, st, a);
   }
-  return accum ? launch_gemv_inst<MAXM, GPW, 0, true, BOOK>(grid, threads, lds, st, a)
-               : launch_gemv_inst<MAXM, GPW, 0, false, BOOK>(grid, threads, lds, st, a);
+  return accum ? launch_gemv_inst<MAXM, GPW, 0, true, BOOK, PAIR>(grid, threads, lds, st, a)
+               : launch_gemv_inst<MAXM, GPW, 0, false, BOOK, PAIR>(grid, threads, lds, st, a);
 }
 
-template <int MAXM, int GPW>
+template <int MAXM, int GPW, bool PAIR = false>
 static int launch_gemv(int book, int sd, int accum, dim3 grid, int threads, size_t lds, hipStream_t st,
                        const GemvArgs &a) {
   switch (book) {
-    case kInt15: return launch_gemv_acc<MAXM, GPW, kInt15>(sd, accum, grid, threads, lds, st, a);
-    case kInt16: return launch_gemv_acc<MAXM, GPW, kInt16>(sd, accum, grid, threads, lds, st, a);
-    case kFp4: return launch_gemv_acc<MAXM, GPW, kFp4>(sd, accum, grid, threads, lds, st, a);
-    default: return launch_gemv_acc<MAXM, GPW, kAffine>(sd, accum, grid, threads, lds, st, a);
+    case kInt15: return launch_gemv_acc<MAXM, GPW, kInt15, PAIR>(sd, accum, grid, threads, lds, st, a);
+    case kInt16: return launch_gemv_acc<MAXM, GPW, kInt16, PAIR>(sd, accum, grid, threads, lds, st, a);
+    case kFp4: return launch_gemv_acc<MAXM, GPW, kFp4, PAIR>(sd, accum, grid, threads, lds, st, a);
+    default: return launch_gemv_acc<MAXM, GPW, kAffine, PAIR>(sd, accum, grid, threads, lds, st, a);
   }
 }
 
@@ -354,8 +424,9 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
                    : gpw == 12 ? launch_gemv<1, 12>(book, sd, accum, grid, threads, lds, st, a)
                    : gpw == 16 ? launch_gemv<1, 16>(book, sd, accum, grid, threads, lds, st, a)
                                : launch_gemv<1, 24>(book, sd, accum, grid, threads, lds, st, a);
-  else rc = gpw == 8    ? launch_gemv<kGemvMaxM, 8>(book, sd, accum, grid, threads, lds, st, a)
-            : gpw == 12 ? launch_gemv<kGemvMaxM, 12>(book, sd, accum, grid, threads, lds, st, a)
+  else if (gpw == 8)   // two tiles per workgroup
+    rc = launch_gemv<kGemvMaxM, 8, true>(book, sd, accum, dim3((tiles_of(N) + 1) / 2), threads, 2 * lds, st, a);
+  else rc = gpw == 12 ? launch_gemv<kGemvMaxM, 12>(book, sd, accum, grid, threads, lds, st, a)
             : gpw == 16 ? launch_gemv<kGemvMaxM, 16>(book, sd, accum, grid, threads, lds, st, a)
                         : launch_gemv<kGemvMaxM, 24>(book, sd, accum, grid, threads, lds, st, a);
   if (rc) return rc;

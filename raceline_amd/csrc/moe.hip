@@ -278,8 +278,12 @@ template <int GPW, int SD, int KIND>
 __global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int item = blockIdx.y;
-  if (item >= *a.n_items) return;               // uniform: the whole workgroup leaves
+  // the item entry is read together with the count (the list holds the most items a call
+  // can have, so the read is in bounds; entries past the count are not used)
   const int4 it = a.items[item];
+  const int n_items = *a.n_items;
+  asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
+  if (item >= n_items) return;                  // uniform: the whole workgroup leaves
   const int e = it.x, r0 = it.y, rows = it.z;
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -337,8 +341,12 @@ template <int GPW, int SD, int KIND, int CPL>
 __global__ __launch_bounds__(1024) void moe_expert_lds_kernel(MoeArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int item = blockIdx.y;
-  if (item >= *a.n_items) return;               // uniform: the whole workgroup leaves
+  // the item entry is read together with the count (the list holds the most items a call
+  // can have, so the read is in bounds; entries past the count are not used)
   const int4 it = a.items[item];
+  const int n_items = *a.n_items;
+  asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
+  if (item >= n_items) return;                  // uniform: the whole workgroup leaves
   const int e = it.x, r0 = it.y, rows = it.z;
   const int tid = threadIdx.x, nthreads = blockDim.x;
   const int lane = tid & 63;

@@ -227,8 +227,40 @@ def bench_prefill(device, steps, warmup):
     log(f"[bench] 27B prefill: {flops / tp / 1e12:.1f} TFLOP/s")
     del rp, l27
     torch.cuda.empty_cache()
+    ref = dense_fp16_reference(device, CFG3_27B, CFG4_PREFILL_M)
+    log(f"[bench] dense fp16 vendor GEMM on the same shapes: {flops / ref / 1e12:.1f} TFLOP/s")
     return {"prefill_27b_m2048": {"us_per_step": round(tp * 1e6, 1), "TFLOP/s": round(flops / tp / 1e12, 1),
-                                  "frac_of_mfma_peak": round(flops / tp / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}}
+                                  "frac_of_mfma_peak": round(flops / tp / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                                  "dense_fp16_vendor_gemm_TFLOP/s": round(flops / ref / 1e12, 1),
+                                  "frac_of_dense_fp16_vendor_gemm": round(ref / tp, 3)}}
+
+
+def dense_fp16_reference(device, shapes, M):
+    """Seconds per layer of the vendor GEMM (torch.nn.functional.linear: y = x W^T with W
+    [N][K] as the packed weights are) on the same shapes with dense fp16 weights and N(0,1)
+    activations: the practical matrix-core ceiling on this box, for comparison only (the
+    quantized path never calls it)."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(7)
+    total = 0.0
+    for _, K, N in shapes:
+        x = torch.randn((M, K), generator=g, device=device, dtype=torch.float16)
+        w = torch.randn((N, K), generator=g, device=device, dtype=torch.float16) * 0.02   # [N][K], as packed
+        for _ in range(3):
+            torch.nn.functional.linear(x, w)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(10):
+            torch.nn.functional.linear(x, w)
+        e.record()
+        torch.cuda.synchronize()
+        total += s.elapsed_time(e) / 10 * 1e-3
+        del x, w
+    torch.cuda.empty_cache()
+    return total
 
 
 def bench_decode(device, steps, warmup):

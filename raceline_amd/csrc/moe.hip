@@ -336,9 +336,14 @@ __global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
 // per tile: the same products, so the two kernels give the same bits.) LDS: 16 rows of
 // K + 8 halves (the pad keeps the 16 rows of an operand read in distinct banks), the
 // group sums [G][16] floats, then the partials of parts 1.. of every tile. CPL: chunks of
-// 8 halves per lane and row (K / 512, rounded up).
-template <int GPW, int SD, int KIND, int CPL>
-__global__ __launch_bounds__(1024) void moe_expert_lds_kernel(MoeArgs a) {
+// 8 halves per lane and row (K / 512, rounded up). SUB: a part is summed as SUB sub-parts of
+// GPW / SUB groups (the per-tile kernel's groups per wave), added in sub-part order, so the
+// sums are the per-tile kernel's. Up to K = 2048 (CPL <= 4) the kernel is held to 80 VGPRs (six
+// waves per SIMD), which lets two 12-wave workgroups share a CU; at K = 4096 LDS allows one
+// workgroup per CU and the registers are left free.
+template <int GPW, int SD, int KIND, int CPL, int SUB>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 6 : 1))) void moe_expert_lds_kernel(
+    MoeArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int item = blockIdx.y;
   // the item entry is read together with the count (the list holds the most items a call
@@ -411,15 +416,32 @@ __global__ __launch_bounds__(1024) void moe_expert_lds_kernel(MoeArgs a) {
     if (c16 == 0) *reinterpret_cast<f32x4 *>(gsl + (size_t)g * 16 + 4 * j4) = gsv;
   }
   __syncthreads();
-  // 5. products, then the parts of each tile meet in part order
-  f32x4 acc = tile_dot_lds<GPW, SD>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn, lane);
-  if (part > 0) red[((size_t)tt * (W - 1) + part - 1) * 64 + lane] = acc;
+  // 5. products, then the sub-parts of each tile meet in order (only those with groups)
+  f32x4 accs[SUB];
+  tile_dot_lds<GPW, SD, SUB>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn, lane, accs);
+  constexpr int per = GPW / SUB;
+  if (part > 0) {
+#pragma unroll
+    for (int s = 0; s < SUB; ++s) red[(((size_t)tt * (W - 1) + part - 1) * SUB + s) * 64 + lane] = accs[s];
+  }
   __syncthreads();
   if (part != 0 || !tile_ok) return;
-  for (int p = 1; p < W; ++p) {
-    const f32x4 o = red[((size_t)tt * (W - 1) + p - 1) * 64 + lane];
+  f32x4 acc = accs[0];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] += o[v];
+  for (int s = 1; s < SUB; ++s) {
+    if (s * per < G) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] += accs[s][v];
+    }
+  }
+  for (int p = 1; p < W; ++p) {
+#pragma unroll
+    for (int s = 0; s < SUB; ++s) {
+      if ((p * SUB + s) * per >= G) break;
+      const f32x4 o = red[(((size_t)tt * (W - 1) + p - 1) * SUB + s) * 64 + lane];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] += o[v];
+    }
   }
   if constexpr (KIND == 0) {
     _Float16 *act = static_cast<_Float16 *>(a.out);
@@ -468,7 +490,10 @@ __global__ void moe_combine_kernel(const float *y, int y_stride, const int *inv,
 
 // ------------------------------------------------------------------ host side
 
-static int expert_gpw(int K) { return 4 * quads_of(K) <= 16 * 16 ? 16 : 24; }
+// Groups per wave of the per-tile kernel: 8 up to K = 2048 (more waves per tile: measured
+// 26.2 -> 23.8 us per MoE layer at T = 1 with H = 2048), then 16, then 24. The staged kernel
+// sums in sub-parts of this many groups, so both give the same bits.
+static int expert_gpw(int K) { return K <= 2048 ? 8 : 4 * quads_of(K) <= 16 * 16 ? 16 : 24; }
 static int expert_waves(int K) { const int g = expert_gpw(K); return (4 * quads_of(K) + g - 1) / g; }
 
 template <int GPW, int SD, int KIND>
@@ -494,33 +519,34 @@ static int staged_gpw(int K) { return K <= 1024 ? 8 : 16; }
 // groups per wave (about 52 VGPRs) two workgroups of 16 waves fit. Measured on the MoE
 // layer at T = 512 (H = 2048, I = 512): gate/up 206 -> 184 us per layer going from 16 to
 // 12 waves; 8 and 16 waves for down within 2 us.
-static int staged_waves(int gpw, size_t lds_bytes) {
-  return gpw == 16 && 2 * lds_bytes <= kMaxLdsBytes ? 12 : 16;
+static int staged_waves(int gpw, int W, int sub, size_t lds_rows) {
+  const size_t lds12 = lds_rows + (size_t)(12 / W) * (W - 1) * sub * 64 * 16;   // a 12-wave workgroup
+  return gpw == 16 && 2 * lds12 <= kMaxLdsBytes ? 12 : 16;
 }
 
-template <int GPW, int SD, int KIND>
+template <int GPW, int SD, int KIND, int SUB>
 static int launch_staged_inst(int tpe, hipStream_t st, MoeArgs a, int items) {
   const int G = a.K / kGroup, W = (G + GPW - 1) / GPW;
   const size_t lds_rows = (size_t)16 * (a.K + 8) * 2 + (size_t)G * 16 * 4;
-  const int tpb = std::max(1, std::min(tpe, staged_waves(GPW, lds_rows + (size_t)(16 / W) * (W - 1) * 1024) / W));
+  const int tpb = std::max(1, std::min(tpe, staged_waves(GPW, W, SUB, lds_rows) / W));
   a.tiles_per_block = tpb;
   a.waves_per_tile = W;
   const int threads = 64 * W * tpb;
   const int xpt = (a.K / 8 + 63) / 64;   // chunks of 8 halves per lane and row
-  const size_t lds = lds_rows + (size_t)tpb * (W - 1) * 64 * 16;
+  const size_t lds = lds_rows + (size_t)tpb * (W - 1) * SUB * 64 * 16;
   const dim3 grid((tpe + tpb - 1) / tpb, items);
   static LdsOptIn lds_opt[4];
-  const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8>)};
+  const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB>)};
   const int which = xpt <= 1 ? 0 : xpt <= 2 ? 1 : xpt <= 4 ? 2 : 3;
   if (xpt <= 8)
     if (int rc = allow_large_lds(fns[which], lds_opt[which])) return rc;
-  if (xpt <= 1) moe_expert_lds_kernel<GPW, SD, KIND, 1><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 2) moe_expert_lds_kernel<GPW, SD, KIND, 2><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 4) moe_expert_lds_kernel<GPW, SD, KIND, 4><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 8) moe_expert_lds_kernel<GPW, SD, KIND, 8><<<grid, threads, lds, st>>>(a);
+  if (xpt <= 1) moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 2) moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 4) moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 8) moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB><<<grid, threads, lds, st>>>(a);
   else return fail("moe: %d activation chunks per thread (K=%d) is more than the staged kernel takes", xpt, a.K);
   RLQ_HIP(hipGetLastError());
   return 0;
@@ -529,13 +555,19 @@ static int launch_staged_inst(int tpe, hipStream_t st, MoeArgs a, int items) {
 template <int KIND>
 static int launch_expert(int K, int sd, int tpe, int items, int tokens, hipStream_t st, const MoeArgs &a) {
   if (K <= kStagedMaxK && tokens >= kStagedMinTokens) {
-    if (staged_gpw(K) == 8) return sd == RLQ_F16 ? launch_staged_inst<8, 0, KIND>(tpe, st, a, items)
-                                                 : launch_staged_inst<8, 1, KIND>(tpe, st, a, items);
-    return sd == RLQ_F16 ? launch_staged_inst<16, 0, KIND>(tpe, st, a, items)
-                         : launch_staged_inst<16, 1, KIND>(tpe, st, a, items);
+    // sub-parts of the per-tile kernel's groups per wave (staged_gpw is a multiple of it)
+    const int sub = staged_gpw(K) / expert_gpw(K);
+    if (staged_gpw(K) == 8) return sd == RLQ_F16 ? launch_staged_inst<8, 0, KIND, 1>(tpe, st, a, items)
+                                                 : launch_staged_inst<8, 1, KIND, 1>(tpe, st, a, items);
+    if (sub == 2) return sd == RLQ_F16 ? launch_staged_inst<16, 0, KIND, 2>(tpe, st, a, items)
+                                       : launch_staged_inst<16, 1, KIND, 2>(tpe, st, a, items);
+    return sd == RLQ_F16 ? launch_staged_inst<16, 0, KIND, 1>(tpe, st, a, items)
+                         : launch_staged_inst<16, 1, KIND, 1>(tpe, st, a, items);
   }
   const dim3 grid(tpe, items);
   const int gpw = expert_gpw(K), threads = 64 * expert_waves(K);
+  if (gpw == 8) return sd == RLQ_F16 ? launch_expert_inst<8, 0, KIND>(grid, threads, st, a)
+                                     : launch_expert_inst<8, 1, KIND>(grid, threads, st, a);
   if (gpw == 16) return sd == RLQ_F16 ? launch_expert_inst<16, 0, KIND>(grid, threads, st, a)
                                       : launch_expert_inst<16, 1, KIND>(grid, threads, st, a);
   return sd == RLQ_F16 ? launch_expert_inst<24, 0, KIND>(grid, threads, st, a)

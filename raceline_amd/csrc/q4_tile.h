@@ -309,25 +309,29 @@ __device__ __forceinline__ void tile_dot_rows2(const WaveTile &w0, const WaveTil
 // times 16 token rows staged in LDS in operand order, with their group sums formed
 // beforehand (group_sums): xs points at row 0's element 64 * wg0 (the wave's first group),
 // rows rstride halves apart; gs at the sums of group wg0, 16 floats (row order) per group.
-// Lane (c16, j4) reads row c16.
-template <int GPW, int SD>
-__device__ __forceinline__ f32x4 tile_dot_lds(const u32x4 (&wq)[GPW / 2], const u32x4 (&sq)[GPW / 4],
-                                              const _Float16 *xs, const float *gs, int rstride, int wn, int lane) {
+// Lane (c16, j4) reads row c16. The part is summed as SUB consecutive sub-parts of GPW / SUB
+// groups, each in its own accumulator (acc[s], from zero), which is how a kernel with
+// GPW / SUB groups per wave sums the same groups.
+template <int GPW, int SD, int SUB>
+__device__ __forceinline__ void tile_dot_lds(const u32x4 (&wq)[GPW / 2], const u32x4 (&sq)[GPW / 4],
+                                             const _Float16 *xs, const float *gs, int rstride, int wn, int lane,
+                                             f32x4 (&acc)[SUB]) {
   const _Float16 *xa = xs + (lane & 15) * rstride + 8 * (lane >> 4);
   const float *ga = gs + 4 * (lane >> 4);
-  f32x4 acc = {};
+#pragma unroll
+  for (int s = 0; s < SUB; ++s) acc[s] = f32x4{};
 #pragma unroll
   for (int jg = 0; jg < GPW; ++jg) {
     if (jg < wn) {   // uniform: the groups past the wave's range add nothing
+      constexpr int per = GPW / SUB;
       half8 af[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(xa + jg * kGroup + 32 * s);
       const f32x4 gsv = *reinterpret_cast<const f32x4 *>(ga + 16 * jg);
-      group_step_gs<GPW, SD, 4>(acc, af, gsv, wq, sq, jg);
-      asm volatile("" : "+v"(acc));
+      group_step_gs<GPW, SD, 4>(acc[jg / per], af, gsv, wq, sq, jg);
+      asm volatile("" : "+v"(acc[jg / per]));
     }
   }
-  return acc;
 }
 
 // Waves 1.. of the workgroup hand their partials to wave 0, which adds them in wave order

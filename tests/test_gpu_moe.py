@@ -184,15 +184,18 @@ def test_layer_full_size_batch_invariance(gpu):
     O.check_close(h.cpu().numpy()[toks].astype(np.float64), ref, TOL, "moe full-size sampled tokens")
 
 
-def test_token_result_same_across_kernel_choice(gpu):
+@pytest.mark.parametrize("E,H,I", [(64, 2048, 512), (16, 1024, 1536), (16, 1536, 1024), (16, 4096, 256)])
+def test_token_result_same_across_kernel_choice(gpu, E, H, I):
     """Calls of fewer than 8 tokens run the per-tile expert kernel, larger ones the kernel
     that stages each item's rows in LDS; a token's result must not depend on which one
-    ran: tokens 3..7 alone (per-tile) give the same bits as inside a 40-token call."""
+    ran: tokens 3..7 alone (per-tile) give the same bits as inside a 40-token call. The
+    shapes cover K (H for gate/up, I for down) where the staged kernel's waves take one
+    (512, 1024, 4096) and two (1536, 2048) of the per-tile kernel's group ranges."""
     import torch
 
     from raceline_amd import ops
 
-    E, topk, H, I = 64, 8, 2048, 512
+    topk = 8
     gu, dn = make_moe(90, E, H, I)
     mw = upload_moe(gu, dn, E, H, I, "f16", gpu)
     x, logits = make_inputs(91, 40, E, H)

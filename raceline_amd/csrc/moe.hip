@@ -33,6 +33,8 @@ constexpr int kItemRows = 16;     // rows per work item: the MFMA tile height
 constexpr int kMaxTopk = 16;
 constexpr int kMaxExperts = 1023; // E; E + 1 <= 1024 (one thread per expert in the sort)
 constexpr int kRouteSmallTokens = 16;   // up to this many tokens route in one launch (a wave each)
+constexpr size_t kSortSmallLds = (2 * 1024 + 32) * 4;
+constexpr int kDownCombineTokens = 4;   // up to this many tokens, rlq_moe runs down + combine as one launch
 
 // Most work items a call can have: sum over experts of ceil(rows_e / 16) <= A / 16 + the
 // number of experts with rows, which is at most min(E + 1, A).
@@ -240,20 +242,57 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int *sel, int T, i
   sort_assignments(sel, T, E, S, wpe, tok, inv, items, n_items, lds);
 }
 
+// The sort for a few assignments (A <= 1024, one thread each): an assignment's row within its
+// expert is the number of earlier assignments to the same expert (a token picks an expert
+// at most once, so this is token order, as sort_assignments places them); an expert's count
+// is a loop over the assignments. One scan gives both the row offsets and the work items
+// (count in the low, item count in the high 16 bits: A <= 1024 keeps both sums in range).
+// LDS: sel [1024] ints, offsets [1024], scan scratch [32].
+__device__ void sort_small(const int *sel, int T, int E, int S, int *tok, int *inv, int4 *items, int *n_items,
+                           unsigned char *lds) {
+  int *sl = reinterpret_cast<int *>(lds);       // [1024]
+  int *off = sl + 1024;                         // [1024]
+  int *scratch = off + 1024;                    // [32]
+  const int tid = threadIdx.x;
+  const int A = T * S, E1 = E + 1;
+  const int ea = tid < A ? min(max(sel[tid], 0), E) : -1;
+  sl[tid] = ea;
+  __syncthreads();
+  int c = 0;
+  if (tid < E1)
+    for (int b = 0; b < A; ++b) c += sl[b] == tid;
+  int rank = 0;
+  for (int b = 0; b < min(tid, A); ++b) rank += sl[b] == ea;
+  const int ni = (c + kItemRows - 1) / kItemRows;
+  const int packed = block_exclusive_scan(c | (ni << 16), scratch, scratch + 16);
+  const int o = packed & 0xFFFF, io = packed >> 16;
+  if (tid < E1) {
+    off[tid] = o;
+    for (int i = 0; i < ni; ++i) items[io + i] = int4{tid, o + i * kItemRows, min(kItemRows, c - i * kItemRows), 0};
+  }
+  if (tid == 0) *n_items = scratch[16] >> 16;
+  __syncthreads();
+  if (tid < A) {
+    const int pos = off[ea] + rank;
+    inv[tid] = pos;
+    tok[pos] = tid / S;
+  }
+}
+
 // Routing of up to 16 tokens in one launch: wave t picks token t's experts, then the whole
-// workgroup sorts (the same steps as moe_topk_kernel followed by moe_sort_kernel; sel and w
+// workgroup sorts them (sort_small: the same rows and items as moe_sort_kernel). sel and w
 // are written to memory and read back after the barrier, which makes them visible to the
-// workgroup).
+// workgroup.
 template <int EPL>
 __global__ __launch_bounds__(1024) void moe_route_small_kernel(const float *logits, int stride, int T, int E, int topk,
-                                                               int norm_topk, int wpe, int *sel, float *w, int *tok,
-                                                               int *inv, int4 *items, int *n_items) {
+                                                               int norm_topk, int *sel, float *w, int *tok, int *inv,
+                                                               int4 *items, int *n_items) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int t = threadIdx.x >> 6;
   const size_t a0 = (size_t)t * (topk + 1);
   if (t < T) topk_token<EPL>(logits + (size_t)t * stride, E, topk, norm_topk, sel + a0, w + a0, threadIdx.x & 63);
   __syncthreads();
-  sort_assignments(sel, T, E, topk + 1, wpe, tok, inv, items, n_items, lds);
+  sort_small(sel, T, E, topk + 1, tok, inv, items, n_items, lds);
 }
 
 // ------------------------------------------------------------------ grouped expert matmuls
@@ -462,6 +501,53 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
   }
 }
 
+// Down projection and combine in one launch, for a few tokens whose items fit one wave's
+// groups (K = I <= 64 * GPW): one workgroup per 16-feature tile of H; wave w takes items
+// w, w + waves, ... and forms the tile's outputs for each item's rows exactly as
+// moe_expert_kernel does (one wave per tile there too); the outputs meet in LDS by row, and
+// the workgroup then adds each token's S slots into its residual row in slot order, with
+// moe_combine_kernel's fused multiply-adds. Same bits as the two launches, without the
+// second one and without writing y. LDS: [A rows][16] floats.
+template <int GPW, int SD>
+__global__ __launch_bounds__(1024) void moe_down_combine_kernel(MoeArgs a, const int *inv, const float *w, int T,
+                                                                int S, float *h, int h_stride) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  float *ys = reinterpret_cast<float *>(lds);
+  const int n_items = *a.n_items;
+  const int waves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, j4 = lane >> 4;
+  const int G = a.K / kGroup, G4 = quads_of(a.K);
+  const int tile = blockIdx.x;
+  const int wn = min(G, GPW);
+  const uint32_t xrange = (uint32_t)((a.x_rows - 1) * a.x_stride + wn * kGroup) * 2u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, xrange);
+  for (int item = wave; item < n_items; item += waves) {
+    const int4 it = a.items[item];
+    const int e = it.x, r0 = it.y, rows = it.z;
+    const WaveTile wt = wave_tile(a.codes, a.sb, e * a.tiles_per_expert + tile, G4, 0, GPW);
+    const bool live = c16 < rows;
+    const int xrow = r0 + (live ? c16 : 0);
+    const f32x4 acc = tile_dot_rows<GPW, SD>(wt, rx, (uint32_t)xrow * a.x_stride * 2u + 16u * j4, live, wn, lane);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = 4 * j4 + v;
+      if (r < rows) ys[(size_t)(r0 + r) * 16 + c16] = acc[v];
+    }
+  }
+  __syncthreads();
+  const int t = threadIdx.x >> 4, c = threadIdx.x & 15;
+  if (t < T) {
+    float acc = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      const int as = t * S + s;
+      acc = __builtin_fmaf(w[as], ys[(size_t)inv[as] * 16 + c], acc);
+    }
+    h[(size_t)t * h_stride + 16 * tile + c] += acc;
+  }
+}
+
 // ------------------------------------------------------------------ combine
 
 // h[t][d] += sum over slots s of w[t*S + s] * y[inv[t*S + s]][d], the slots in order
@@ -610,19 +696,11 @@ int rlq_moe_route(const float *logits, int logit_stride, int T, int E, int topk,
   const int wpe = sort_wpe(E);
   const size_t lds = sort_lds_bytes(E, wpe);
   if (T <= kRouteSmallTokens) {
-    // one launch: the top-k of each token by its own wave, then the sort
-    static LdsOptIn small_opt[5];
-    const int which = epl <= 1 ? 0 : epl <= 2 ? 1 : epl <= 4 ? 2 : epl <= 8 ? 3 : 4;
-    const void *fns[5] = {reinterpret_cast<const void *>(&moe_route_small_kernel<1>),
-                          reinterpret_cast<const void *>(&moe_route_small_kernel<2>),
-                          reinterpret_cast<const void *>(&moe_route_small_kernel<4>),
-                          reinterpret_cast<const void *>(&moe_route_small_kernel<8>),
-                          reinterpret_cast<const void *>(&moe_route_small_kernel<16>)};
-    if (int rc = allow_large_lds(fns[which], small_opt[which])) return rc;
+    // one launch: the top-k of each token by its own wave, then the sort (8 KB of LDS)
     int4 *it4 = reinterpret_cast<int4 *>(items);
 #define RLQ_ROUTE_SMALL(N)                                                                                             \
-  moe_route_small_kernel<N><<<1, 1024, lds, st>>>(logits, logit_stride, T, E, topk, norm_topk, wpe, sel, w, tok, inv, \
-                                                  it4, n_items)
+  moe_route_small_kernel<N><<<1, 1024, kSortSmallLds, st>>>(logits, logit_stride, T, E, topk, norm_topk, sel, w, tok,  \
+                                                            inv, it4, n_items)
     if (epl <= 1) RLQ_ROUTE_SMALL(1);
     else if (epl <= 2) RLQ_ROUTE_SMALL(2);
     else if (epl <= 4) RLQ_ROUTE_SMALL(4);
@@ -752,6 +830,28 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
   if (int rc = rlq_moe_gate_up(x, x_stride, T, H, I, E, topk, packed_gu, scale_dtype, tok, items, n_items, act, I,
                                stream))
     return rc;
+  if (T <= kDownCombineTokens && expert_gpw(I) == 8 && I / kGroup <= 8) {
+    // a few tokens: down and combine in one launch (the same bits as the two below)
+    RLQ_REQUIRE(h && h_stride >= H, "rlq_moe: h is null or h_stride=%d < H=%d", h_stride, H);
+    MoeArgs a = {};
+    a.x = act;
+    a.codes = static_cast<const u32x4 *>(packed_dn);
+    a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed_dn) + packed_code_bytes(I, (E + 1) * H));
+    a.items = reinterpret_cast<const int4 *>(items);
+    a.n_items = n_items;
+    a.x_rows = (int)A;
+    a.x_stride = I;
+    a.K = I;
+    a.tiles_per_expert = H / 16;
+    const int waves = (int)std::min<size_t>(16, A);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (scale_dtype == RLQ_F16)
+      moe_down_combine_kernel<8, 0><<<H / 16, 64 * waves, A * 16 * 4, st>>>(a, inv, w, T, topk + 1, h, h_stride);
+    else
+      moe_down_combine_kernel<8, 1><<<H / 16, 64 * waves, A * 16 * 4, st>>>(a, inv, w, T, topk + 1, h, h_stride);
+    RLQ_HIP(hipGetLastError());
+    return 0;
+  }
   if (int rc = rlq_moe_down(act, I, T, H, I, E, topk, packed_dn, scale_dtype, items, n_items, y, H, stream)) return rc;
   return rlq_moe_combine(y, H, inv, w, T, topk, H, h, h_stride, stream);
 }

@@ -114,7 +114,8 @@ def test_gate_up_swiglu_and_down(gpu, sd):
     O.check_close(y_g, y_ref, TOL, f"moe down ({sd})")
 
 
-@pytest.mark.parametrize("T,E,topk,H,I", [(1, 16, 4, 256, 128), (33, 32, 4, 512, 256), (5, 256, 8, 2048, 512)])
+@pytest.mark.parametrize("T,E,topk,H,I", [(1, 16, 4, 256, 128), (33, 32, 4, 512, 256), (5, 256, 8, 2048, 512),
+                                           (4, 64, 8, 512, 512), (2, 16, 4, 256, 1024)])
 def test_layer_matches_oracle(gpu, T, E, topk, H, I):
     import torch
 
@@ -203,8 +204,12 @@ def test_token_result_same_across_kernel_choice(gpu, E, H, I):
     ops.moe(to_dev(x, gpu), to_dev(logits, gpu), mw, topk, h)
     h5 = torch.zeros((5, H), dtype=torch.float32, device=gpu)
     ops.moe(to_dev(x[3:8].copy(), gpu), to_dev(logits[3:8].copy(), gpu), mw, topk, h5)
+    # up to 4 tokens also fold the combine into the down launch
+    h3 = torch.zeros((3, H), dtype=torch.float32, device=gpu)
+    ops.moe(to_dev(x[3:6].copy(), gpu), to_dev(logits[3:6].copy(), gpu), mw, topk, h3)
     _sync()
     assert torch.equal(h5, h[3:8])
+    assert torch.equal(h3, h[3:6])
     ref, _, _ = O.moe_layer_f64(x[3:8], logits[3:8], gu, dn, E, topk, I, H)
     O.check_close(h5.cpu().numpy().astype(np.float64), ref, TOL, "moe per-tile vs staged")
 

@@ -311,19 +311,12 @@ struct MoeArgs {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
-// KIND 0: gate/up with the gather and SwiGLU fused (interleaved stack); KIND 1: down.
-// grid (tiles_per_expert, max_items); block 64 * ceil(4 G4 / GPW).
-template <int GPW, int SD, int KIND>
-__global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  const int item = blockIdx.y;
-  // the item entry is read together with the count (the list holds the most items a call
-  // can have, so the read is in bounds; entries past the count are not used)
-  const int4 it = a.items[item];
-  const int n_items = *a.n_items;
-  asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
-  if (item >= n_items) return;                  // uniform: the whole workgroup leaves
-  const int e = it.x, r0 = it.y, rows = it.z;
+// One item's products for one 16-row weight tile (tile = blockIdx.x) by all the workgroup's
+// waves, each a range of GPW groups of K; the waves meet in LDS in wave order and wave 0
+// writes. KIND 0: gate/up with the gather and SwiGLU fused (interleaved stack); the rows'
+// tokens come from the row -> token map, or (ONE_TOKEN) are all token 0. KIND 1: down.
+template <int GPW, int SD, int KIND, bool ONE_TOKEN>
+__device__ __forceinline__ void expert_tile(const MoeArgs &a, int e, int r0, int rows, unsigned char *lds) {
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -337,7 +330,7 @@ __global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
 
   const bool live = c16 < rows;
   int xrow = r0 + (live ? c16 : 0);
-  if constexpr (KIND == 0) xrow = a.tok[xrow];
+  if constexpr (KIND == 0) xrow = ONE_TOKEN ? 0 : a.tok[xrow];
   const uint32_t xrange = wn > 0 ? (uint32_t)((a.x_rows - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
   f32x4 acc = tile_dot_rows<GPW, SD>(wt, rx, (uint32_t)xrow * a.x_stride * 2u + 16u * j4, live, wn, lane);
@@ -361,6 +354,58 @@ __global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
       if (r < rows) y[(size_t)(r0 + r) * a.out_stride + 16 * tile + c16] = acc[v];
     }
   }
+}
+
+// grid (tiles_per_expert, max_items); block 64 * ceil(4 G4 / GPW).
+template <int GPW, int SD, int KIND>
+__global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int item = blockIdx.y;
+  // the item entry is read together with the count (the list holds the most items a call
+  // can have, so the read is in bounds; entries past the count are not used)
+  const int4 it = a.items[item];
+  const int n_items = *a.n_items;
+  asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
+  if (item >= n_items) return;                  // uniform: the whole workgroup leaves
+  expert_tile<GPW, SD, KIND, false>(a, it.x, it.y, it.z, lds);
+}
+
+// One token: its routing and the gate/up products in one launch. Every workgroup picks the
+// token's experts itself (wave 0, topk_token, as moe_topk_kernel does) and takes its item
+// from them: with one token each chosen expert has one row, and the sort orders experts by
+// number, so item i (= blockIdx.y, S of them) is the i-th smallest chosen expert, at row i.
+// Workgroup (0, 0) also writes the routing tables (sel, w, tok, inv, items, n_items) as the
+// sort writes them for one token, for the down and combine launch. LDS: the reduction, then
+// sel [S] and w [S].
+template <int GPW, int SD, int EPL>
+__global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, const float *logits, int E, int topk,
+                                                                     int norm_topk, int *sel, float *w, int *tok,
+                                                                     int *inv, int4 *items, int *n_items) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int S = topk + 1;
+  const int waves = blockDim.x >> 6;
+  int *sel_l = reinterpret_cast<int *>(lds + (size_t)(waves - 1) * 64 * 16);
+  float *w_l = reinterpret_cast<float *>(sel_l + S);
+  if (threadIdx.x < 64) topk_token<EPL>(logits, E, topk, norm_topk, sel_l, w_l, threadIdx.x);
+  __syncthreads();
+  // slot s's expert has rank s_rank among the S distinct chosen experts
+  const int i = blockIdx.y;
+  int e = 0;
+  for (int s = 0; s < S; ++s) {
+    const int es = sel_l[s];
+    int rank = 0;
+    for (int q = 0; q < S; ++q) rank += sel_l[q] < es;
+    if (rank == i) e = es;
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+      sel[s] = es;
+      w[s] = w_l[s];
+      inv[s] = rank;
+      tok[rank] = 0;
+      items[rank] = int4{es, rank, 1, 0};
+    }
+  }
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *n_items = S;
+  expert_tile<GPW, SD, 0, true>(a, e, i, 1, lds);
 }
 
 // The same products with the item's token rows staged once per workgroup: a workgroup
@@ -674,6 +719,68 @@ static int check_moe_shape(const char *fn, int T, int E, int topk, int H, int I)
   return 0;
 }
 
+// The argument checks and kernel arguments of rlq_moe_gate_up.
+static int gate_up_args(const void *x, int x_stride, int T, int H, int I, int E, int topk, const void *packed_gu,
+                        int scale_dtype, const int *tok, const int *items, const int *n_items, void *act,
+                        int act_stride, MoeArgs &a) {
+  if (int rc = check_moe_shape("rlq_moe_gate_up", T, E, topk, H, I)) return rc;
+  RLQ_REQUIRE(scale_dtype == RLQ_F16 || scale_dtype == RLQ_BF16, "rlq_moe_gate_up: unknown scale dtype %d", scale_dtype);
+  RLQ_REQUIRE(x && packed_gu && tok && items && n_items && act, "rlq_moe_gate_up: null pointer argument");
+  RLQ_REQUIRE(x_stride >= H && x_stride % 8 == 0 && aligned(x, 16), "rlq_moe_gate_up: x must be 16-byte aligned "
+              "with x_stride >= H and a multiple of 8 (got %d)", x_stride);
+  RLQ_REQUIRE(act_stride >= I && aligned(act, 2), "rlq_moe_gate_up: act_stride=%d < I=%d", act_stride, I);
+  RLQ_REQUIRE((long long)T * x_stride * 2 < (1LL << 31), "rlq_moe_gate_up: x spans more than 2 GiB");
+  RLQ_REQUIRE(aligned(packed_gu, 16) && aligned(items, 16), "rlq_moe_gate_up: packed and items must be 16-byte aligned");
+  const int N = (E + 1) * 2 * I;
+  a = MoeArgs{};
+  a.x = static_cast<const _Float16 *>(x);
+  a.tok = tok;
+  a.codes = static_cast<const u32x4 *>(packed_gu);
+  a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed_gu) + packed_code_bytes(H, N));
+  a.items = reinterpret_cast<const int4 *>(items);
+  a.n_items = n_items;
+  a.out = act;
+  a.x_rows = T;
+  a.x_stride = x_stride;
+  a.K = H;
+  a.tiles_per_expert = 2 * I / 16;
+  a.out_stride = act_stride;
+  return 0;
+}
+
+// One token, routing and gate/up in one launch (moe_gate_up_one_token_kernel); returns 1
+// when the shape has no such kernel (E > 256 or K past 16 groups per wave), and the caller
+// routes and multiplies in two launches.
+template <int GPW, int SD, int EPL>
+static void launch_one_token_inst(const MoeArgs &a, const float *logits, int E, int topk, int norm_topk, int *sel,
+                                  float *w, int *tok, int *inv, int *items, int *n_items, hipStream_t st) {
+  const int waves = expert_waves(a.K), S = topk + 1;
+  const size_t lds = (size_t)(waves - 1) * 64 * 16 + (size_t)S * 8;
+  moe_gate_up_one_token_kernel<GPW, SD, EPL><<<dim3(a.tiles_per_expert, S), 64 * waves, lds, st>>>(
+      a, logits, E, topk, norm_topk, sel, w, tok, inv, reinterpret_cast<int4 *>(items), n_items);
+}
+
+template <int GPW, int SD>
+static int launch_one_token_epl(int epl, const MoeArgs &a, const float *logits, int E, int topk, int norm_topk,
+                                int *sel, float *w, int *tok, int *inv, int *items, int *n_items, hipStream_t st) {
+  if (epl <= 1) launch_one_token_inst<GPW, SD, 1>(a, logits, E, topk, norm_topk, sel, w, tok, inv, items, n_items, st);
+  else if (epl <= 2) launch_one_token_inst<GPW, SD, 2>(a, logits, E, topk, norm_topk, sel, w, tok, inv, items, n_items, st);
+  else launch_one_token_inst<GPW, SD, 4>(a, logits, E, topk, norm_topk, sel, w, tok, inv, items, n_items, st);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+static int route_gate_up_one_token(const MoeArgs &a, int sd, const float *logits, int E, int topk, int norm_topk,
+                                   int *sel, float *w, int *tok, int *inv, int *items, int *n_items, hipStream_t st) {
+  const int epl = (E + 63) / 64, gpw = expert_gpw(a.K);
+  if (epl > 4 || (gpw != 8 && gpw != 16)) return 1;
+  if (gpw == 8)
+    return sd == RLQ_F16 ? launch_one_token_epl<8, 0>(epl, a, logits, E, topk, norm_topk, sel, w, tok, inv, items, n_items, st)
+                         : launch_one_token_epl<8, 1>(epl, a, logits, E, topk, norm_topk, sel, w, tok, inv, items, n_items, st);
+  return sd == RLQ_F16 ? launch_one_token_epl<16, 0>(epl, a, logits, E, topk, norm_topk, sel, w, tok, inv, items, n_items, st)
+                       : launch_one_token_epl<16, 1>(epl, a, logits, E, topk, norm_topk, sel, w, tok, inv, items, n_items, st);
+}
+
 }  // namespace rlq
 
 using namespace rlq;
@@ -727,28 +834,10 @@ int rlq_moe_route(const float *logits, int logit_stride, int T, int E, int topk,
 int rlq_moe_gate_up(const void *x, int x_stride, int T, int H, int I, int E, int topk, const void *packed_gu,
                     int scale_dtype, const int *tok, const int *items, const int *n_items, void *act, int act_stride,
                     void *stream) {
-  if (int rc = check_moe_shape("rlq_moe_gate_up", T, E, topk, H, I)) return rc;
-  RLQ_REQUIRE(scale_dtype == RLQ_F16 || scale_dtype == RLQ_BF16, "rlq_moe_gate_up: unknown scale dtype %d", scale_dtype);
-  RLQ_REQUIRE(x && packed_gu && tok && items && n_items && act, "rlq_moe_gate_up: null pointer argument");
-  RLQ_REQUIRE(x_stride >= H && x_stride % 8 == 0 && aligned(x, 16), "rlq_moe_gate_up: x must be 16-byte aligned "
-              "with x_stride >= H and a multiple of 8 (got %d)", x_stride);
-  RLQ_REQUIRE(act_stride >= I && aligned(act, 2), "rlq_moe_gate_up: act_stride=%d < I=%d", act_stride, I);
-  RLQ_REQUIRE((long long)T * x_stride * 2 < (1LL << 31), "rlq_moe_gate_up: x spans more than 2 GiB");
-  RLQ_REQUIRE(aligned(packed_gu, 16) && aligned(items, 16), "rlq_moe_gate_up: packed and items must be 16-byte aligned");
-  const int N = (E + 1) * 2 * I;
-  MoeArgs a = {};
-  a.x = static_cast<const _Float16 *>(x);
-  a.tok = tok;
-  a.codes = static_cast<const u32x4 *>(packed_gu);
-  a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed_gu) + packed_code_bytes(H, N));
-  a.items = reinterpret_cast<const int4 *>(items);
-  a.n_items = n_items;
-  a.out = act;
-  a.x_rows = T;
-  a.x_stride = x_stride;
-  a.K = H;
-  a.tiles_per_expert = 2 * I / 16;
-  a.out_stride = act_stride;
+  MoeArgs a;
+  if (int rc = gate_up_args(x, x_stride, T, H, I, E, topk, packed_gu, scale_dtype, tok, items, n_items, act, act_stride,
+                            a))
+    return rc;
   return launch_expert<0>(H, scale_dtype, a.tiles_per_expert, moe_max_items(T, E, topk), T,
                           static_cast<hipStream_t>(stream), a);
 }
@@ -825,11 +914,25 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
   int *n_items = reinterpret_cast<int *>(p);        p += 256;
   _Float16 *act = reinterpret_cast<_Float16 *>(p);  p += align256(A * I * 2);
   float *y = reinterpret_cast<float *>(p);
-  if (int rc = rlq_moe_route(logits, logit_stride, T, E, topk, norm_topk, sel, w, tok, inv, items, n_items, stream))
-    return rc;
-  if (int rc = rlq_moe_gate_up(x, x_stride, T, H, I, E, topk, packed_gu, scale_dtype, tok, items, n_items, act, I,
-                               stream))
-    return rc;
+  int fused = 1;
+  if (T == 1) {
+    // one token: routing and gate/up in one launch where a kernel covers the shape
+    RLQ_REQUIRE(logits && logit_stride >= E + 1, "rlq_moe: logits null or logit_stride=%d < E + 1 = %d", logit_stride,
+                E + 1);
+    MoeArgs a;
+    if (int rc = gate_up_args(x, x_stride, T, H, I, E, topk, packed_gu, scale_dtype, tok, items, n_items, act, I, a))
+      return rc;
+    fused = route_gate_up_one_token(a, scale_dtype, logits, E, topk, norm_topk, sel, w, tok, inv, items, n_items,
+                                    static_cast<hipStream_t>(stream));
+    if (fused < 0) return fused;
+  }
+  if (fused) {
+    if (int rc = rlq_moe_route(logits, logit_stride, T, E, topk, norm_topk, sel, w, tok, inv, items, n_items, stream))
+      return rc;
+    if (int rc = rlq_moe_gate_up(x, x_stride, T, H, I, E, topk, packed_gu, scale_dtype, tok, items, n_items, act, I,
+                                 stream))
+      return rc;
+  }
   if (T <= kDownCombineTokens && expert_gpw(I) == 8 && I / kGroup <= 8) {
     // a few tokens: down and combine in one launch (the same bits as the two below)
     RLQ_REQUIRE(h && h_stride >= H, "rlq_moe: h is null or h_stride=%d < H=%d", h_stride, H);

@@ -159,8 +159,15 @@ def test_layer_full_size_batch_invariance(gpu):
     ops.moe(x, logits, mw, topk, h)
     h_sub = torch.zeros((64, H), dtype=torch.float32, device=dev)
     ops.moe(x[100:164].contiguous(), logits[100:164].contiguous(), mw, topk, h_sub)
+    # one token alone (routing inside the gate/up launch, down and combine in one) and three
+    h_one = torch.zeros((1, H), dtype=torch.float32, device=dev)
+    ops.moe(x[163:164].contiguous(), logits[163:164].contiguous(), mw, topk, h_one)
+    h_three = torch.zeros((3, H), dtype=torch.float32, device=dev)
+    ops.moe(x[254:257].contiguous(), logits[254:257].contiguous(), mw, topk, h_three)
     _sync()
     assert torch.equal(h_sub, h[100:164])
+    assert torch.equal(h_one, h[163:164])
+    assert torch.equal(h_three, h[254:257])
 
     # oracle on sampled tokens
     def host(t3):
@@ -204,12 +211,16 @@ def test_token_result_same_across_kernel_choice(gpu, E, H, I):
     ops.moe(to_dev(x, gpu), to_dev(logits, gpu), mw, topk, h)
     h5 = torch.zeros((5, H), dtype=torch.float32, device=gpu)
     ops.moe(to_dev(x[3:8].copy(), gpu), to_dev(logits[3:8].copy(), gpu), mw, topk, h5)
-    # up to 4 tokens also fold the combine into the down launch
+    # up to 4 tokens also fold the combine into the down launch; one token also routes in
+    # the gate/up launch
     h3 = torch.zeros((3, H), dtype=torch.float32, device=gpu)
     ops.moe(to_dev(x[3:6].copy(), gpu), to_dev(logits[3:6].copy(), gpu), mw, topk, h3)
+    h1 = torch.zeros((1, H), dtype=torch.float32, device=gpu)
+    ops.moe(to_dev(x[7:8].copy(), gpu), to_dev(logits[7:8].copy(), gpu), mw, topk, h1)
     _sync()
     assert torch.equal(h5, h[3:8])
     assert torch.equal(h3, h[3:6])
+    assert torch.equal(h1, h[7:8])
     ref, _, _ = O.moe_layer_f64(x[3:8], logits[3:8], gu, dn, E, topk, I, H)
     O.check_close(h5.cpu().numpy().astype(np.float64), ref, TOL, "moe per-tile vs staged")
 

@@ -144,23 +144,33 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int 
 // ------------------------------------------------------------------ routing: sort
 
 // Exclusive prefix sum over the workgroup (1024 threads) of one int per thread.
+// Inclusive prefix sum over the wave: within rows of 16 lanes by DPP row shifts (1, 2, 4,
+// 8; lanes shifted in from outside the row read 0), then each row adds the totals of the
+// rows before it, read as scalars.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+  const int t0 = __builtin_amdgcn_readlane(v, 15), t1 = __builtin_amdgcn_readlane(v, 31),
+            t2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = (threadIdx.x & 63) >> 4;
+  return v + (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
+}
+
+// Exclusive prefix sum over the workgroup (at most 16 waves) of one int per thread; *total
+// gets the sum. wave_tot: 16 ints of LDS.
 __device__ int block_exclusive_scan(int v, int *wave_tot, int *total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inc = v;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(inc, o);
-    if (lane >= o) inc += u;
-  }
+  const int inc = wave_inclusive_scan(v);
   if (lane == 63) wave_tot[wave] = inc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) {
-      const int c = wave_tot[i];
-      wave_tot[i] = run;
-      run += c;
-    }
-    *total = run;
+  if (wave == 0) {
+    const int nw = blockDim.x >> 6;
+    const int t = lane < nw ? wave_tot[lane] : 0;
+    const int ti = wave_inclusive_scan(t);
+    if (lane < nw) wave_tot[lane] = ti - t;
+    if (lane == nw - 1) *total = ti;
   }
   __syncthreads();
   const int ex = wave_tot[wave] + inc - v;
@@ -193,15 +203,24 @@ __device__ void sort_assignments(const int *sel, int T, int E, int S, int wpe, i
   for (int a = tid; a < A; a += 1024) atomicAdd(&cnt[min(max(sel[a], 0), E)], 1);
   __syncthreads();
   const int c = tid < E1 ? cnt[tid] : 0;
-  const int o = block_exclusive_scan(c, scratch, scratch + 16);
   const int ni = (c + kItemRows - 1) / kItemRows;
-  const int io = block_exclusive_scan(ni, scratch, scratch + 17);
+  int o, io, n_it;
+  if (A < (1 << 15)) {   // uniform: counts and item counts fit one scan, 16 bits each
+    const int packed = block_exclusive_scan(c | (ni << 16), scratch, scratch + 16);
+    o = packed & 0xFFFF;
+    io = packed >> 16;
+    n_it = scratch[16] >> 16;
+  } else {
+    o = block_exclusive_scan(c, scratch, scratch + 16);
+    io = block_exclusive_scan(ni, scratch, scratch + 17);
+    n_it = scratch[17];
+  }
   if (tid < E1) {
     off[tid] = o;
     for (int i = 0; i < ni; ++i)
       items[io + i] = int4{tid, o + i * kItemRows, min(kItemRows, c - i * kItemRows), 0};
   }
-  if (tid == 0) *n_items = scratch[17];
+  if (tid == 0) *n_items = n_it;
   __syncthreads();
 
   const int chunk = 32 * wpe;                   // tokens per chunk

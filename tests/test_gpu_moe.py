@@ -58,7 +58,8 @@ def _sync():
 
 @pytest.mark.parametrize("T,E,topk,norm", [(1, 16, 4, True), (7, 16, 4, False), (40, 64, 8, True),
                                            (300, 256, 8, True), (1, 256, 8, True), (2000, 8, 2, True),
-                                           (16, 256, 8, True), (17, 64, 8, False), (16, 700, 16, False)])
+                                           (16, 256, 8, True), (17, 64, 8, False), (16, 700, 16, False),
+                                           (4000, 64, 8, True)])
 def test_route(gpu, T, E, topk, norm):
     from raceline_amd import ops
 

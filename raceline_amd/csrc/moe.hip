@@ -6,9 +6,13 @@
 // expert first) plus the shared expert, number E; S = topk + 1 assignments per token,
 // assignment a = t * S + slot. The routing sorts the assignments by expert into "rows";
 // each expert's rows are consecutive, and an expert's rows are cut into work items of at
-// most 16 rows (the MFMA tile height). The grouped kernels run one workgroup per (item,
-// 16-row weight tile) over the expert's matrices in the stacked tensors; the combine adds
-// each token's S results to its residual row in slot order.
+// most 16 rows (the MFMA tile height). The grouped matmuls run over the expert's matrices
+// in the stacked tensors: below 8 tokens one small workgroup per (item, 16-row weight
+// tile) (moe_expert_kernel), from 8 tokens one workgroup per (item, block of tiles) with
+// the item's rows staged once in LDS (moe_expert_lds_kernel); both give the same bits.
+// The combine adds each token's S results to its residual row in slot order. For one
+// token, rlq_moe routes inside the gate/up launch; up to four tokens, it runs the down
+// projection and the combine as one launch (the same bits as the separate steps).
 //
 // Differences from the reference, all of them MI355X choices:
 //  - rows within an expert are placed in token order (the reference places them with
@@ -654,10 +658,10 @@ static int launch_expert_inst(dim3 grid, int threads, hipStream_t st, const MoeA
   return 0;
 }
 
-// The staged kernel takes K <= kStagedMaxK (its 16 rows of K halves fit LDS with room for a
-// second workgroup per CU) and calls of at least kStagedMinTokens tokens: with fewer, items
-// hold a row or two, there is nothing to reuse, and the per-tile kernel's many small
-// workgroups spread the weight stream over more CUs (measured at T = 1: 31.4 against
+// The staged kernel takes K <= kStagedMaxK (its 16 rows of K halves fit LDS: two workgroups
+// per CU up to K = 2048, one at 4096) and calls of at least kStagedMinTokens tokens: with
+// fewer, items hold a row or two, there is nothing to reuse, and the per-tile kernel's many
+// small workgroups spread the weight stream over more CUs (measured at T = 1: 31.4 against
 // 33.0 us per layer). Groups per wave: 8 up to K = 1024, then 16.
 constexpr int kStagedMaxK = 4096;
 constexpr int kStagedMinTokens = 8;

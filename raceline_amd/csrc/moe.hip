@@ -147,7 +147,6 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int 
 
 // ------------------------------------------------------------------ routing: sort
 
-// Exclusive prefix sum over the workgroup (1024 threads) of one int per thread.
 // Inclusive prefix sum over the wave: within rows of 16 lanes by DPP row shifts (1, 2, 4,
 // 8; lanes shifted in from outside the row read 0), then each row adds the totals of the
 // rows before it, read as scalars.

@@ -398,7 +398,7 @@ __global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
 // number, so item i (= blockIdx.y, S of them) is the i-th smallest chosen expert, at row i.
 // Workgroup (0, 0) also writes the routing tables (sel, w, tok, inv, items, n_items) as the
 // sort writes them for one token, for the down and combine launch. LDS: the reduction, then
-// sel [S] and w [S].
+// sel [S], w [S] and the chosen experts in ascending order [S].
 template <int GPW, int SD, int EPL>
 __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, const float *logits, int E, int topk,
                                                                      int norm_topk, int *sel, float *w, int *tok,
@@ -408,26 +408,28 @@ __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, 
   const int waves = blockDim.x >> 6;
   int *sel_l = reinterpret_cast<int *>(lds + (size_t)(waves - 1) * 64 * 16);
   float *w_l = reinterpret_cast<float *>(sel_l + S);
+  int *order = reinterpret_cast<int *>(w_l + S);   // the chosen experts in ascending order
   if (threadIdx.x < 64) topk_token<EPL>(logits, E, topk, norm_topk, sel_l, w_l, threadIdx.x);
   __syncthreads();
-  // slot s's expert has rank s_rank among the S distinct chosen experts
-  const int i = blockIdx.y;
-  int e = 0;
-  for (int s = 0; s < S; ++s) {
+  // thread s ranks slot s's expert among the S distinct chosen experts
+  const int s = threadIdx.x;
+  if (s < S) {
     const int es = sel_l[s];
     int rank = 0;
     for (int q = 0; q < S; ++q) rank += sel_l[q] < es;
-    if (rank == i) e = es;
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+    order[rank] = es;
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
       sel[s] = es;
       w[s] = w_l[s];
       inv[s] = rank;
       tok[rank] = 0;
       items[rank] = int4{es, rank, 1, 0};
+      if (s == 0) *n_items = S;
     }
   }
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *n_items = S;
-  expert_tile<GPW, SD, 0, true>(a, e, i, 1, lds);
+  __syncthreads();
+  const int i = blockIdx.y;
+  expert_tile<GPW, SD, 0, true>(a, order[i], i, 1, lds);
 }
 
 // The same products with the item's token rows staged once per workgroup: a workgroup
@@ -777,7 +779,7 @@ template <int GPW, int SD, int EPL>
 static void launch_one_token_inst(const MoeArgs &a, const float *logits, int E, int topk, int norm_topk, int *sel,
                                   float *w, int *tok, int *inv, int *items, int *n_items, hipStream_t st) {
   const int waves = expert_waves(a.K), S = topk + 1;
-  const size_t lds = (size_t)(waves - 1) * 64 * 16 + (size_t)S * 8;
+  const size_t lds = (size_t)(waves - 1) * 64 * 16 + (size_t)S * 12;
   moe_gate_up_one_token_kernel<GPW, SD, EPL><<<dim3(a.tiles_per_expert, S), 64 * waves, lds, st>>>(
       a, logits, E, topk, norm_topk, sel, w, tok, inv, reinterpret_cast<int4 *>(items), n_items);
 }

@@ -576,16 +576,29 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
 // moe_expert_kernel does (one wave per tile there too); the outputs meet in LDS by row, and
 // the workgroup then adds each token's S slots into its residual row in slot order, with
 // moe_combine_kernel's fused multiply-adds. Same bits as the two launches, without the
-// second one and without writing y. LDS: [A rows][16] floats.
+// second one and without writing y. LDS: [A rows][16] floats, then inv [A] and w [A].
 template <int GPW, int SD>
 __global__ __launch_bounds__(1024) void moe_down_combine_kernel(MoeArgs a, const int *inv, const float *w, int T,
                                                                 int S, float *h, int h_stride) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   float *ys = reinterpret_cast<float *>(lds);
+  const int A = T * S;
+  const int t = threadIdx.x >> 4, c = threadIdx.x & 15;
+  // Every global read that does not depend on the routing result is issued first, so that
+  // its latency overlaps the weight stream: the wave's first item with the count (the list
+  // holds at least as many entries as there are waves), this thread's routing-table entry
+  // and, for the combining threads, the residual value the sum is added to.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool table = (int)threadIdx.x < A;
+  const int inv_r = table ? inv[threadIdx.x] : 0;
+  const float w_r = table ? w[threadIdx.x] : 0.0f;
+  float *hp = h + (size_t)t * h_stride + 16 * blockIdx.x + c;
+  const float h_r = t < T ? *hp : 0.0f;
+  const int4 it0 = a.items[wave];
   const int n_items = *a.n_items;
+  asm volatile("" ::"s"(it0.x), "s"(it0.y), "s"(it0.z), "s"(n_items));   // both loads before the branch
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c16 = lane & 15, j4 = lane >> 4;
   const int G = a.K / kGroup, G4 = quads_of(a.K);
   const int tile = blockIdx.x;
@@ -593,7 +606,7 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(MoeArgs a, const
   const uint32_t xrange = (uint32_t)((a.x_rows - 1) * a.x_stride + wn * kGroup) * 2u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, xrange);
   for (int item = wave; item < n_items; item += waves) {
-    const int4 it = a.items[item];
+    const int4 it = item == wave ? it0 : a.items[item];
     const int e = it.x, r0 = it.y, rows = it.z;
     const WaveTile wt = wave_tile(a.codes, a.sb, e * a.tiles_per_expert + tile, G4, 0, GPW);
     const bool live = c16 < rows;
@@ -605,15 +618,20 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(MoeArgs a, const
       if (r < rows) ys[(size_t)(r0 + r) * 16 + c16] = acc[v];
     }
   }
+  int *inv_l = reinterpret_cast<int *>(ys + (size_t)A * 16);
+  float *w_l = reinterpret_cast<float *>(inv_l + A);
+  if (table) {
+    inv_l[threadIdx.x] = inv_r;
+    w_l[threadIdx.x] = w_r;
+  }
   __syncthreads();
-  const int t = threadIdx.x >> 4, c = threadIdx.x & 15;
   if (t < T) {
     float acc = 0.0f;
     for (int s = 0; s < S; ++s) {
       const int as = t * S + s;
-      acc = __builtin_fmaf(w[as], ys[(size_t)inv[as] * 16 + c], acc);
+      acc = __builtin_fmaf(w_l[as], ys[(size_t)inv_l[as] * 16 + c], acc);
     }
-    h[(size_t)t * h_stride + 16 * tile + c] += acc;
+    *hp = h_r + acc;
   }
 }
 
@@ -970,12 +988,12 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
     a.x_stride = I;
     a.K = I;
     a.tiles_per_expert = H / 16;
-    const int waves = (int)std::min<size_t>(16, A);
+    const int waves = (int)std::min<size_t>(std::min<size_t>(16, A), moe_max_items(T, E, topk));
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (scale_dtype == RLQ_F16)
-      moe_down_combine_kernel<8, 0><<<H / 16, 64 * waves, A * 16 * 4, st>>>(a, inv, w, T, topk + 1, h, h_stride);
+      moe_down_combine_kernel<8, 0><<<H / 16, 64 * waves, A * 72, st>>>(a, inv, w, T, topk + 1, h, h_stride);
     else
-      moe_down_combine_kernel<8, 1><<<H / 16, 64 * waves, A * 16 * 4, st>>>(a, inv, w, T, topk + 1, h, h_stride);
+      moe_down_combine_kernel<8, 1><<<H / 16, 64 * waves, A * 72, st>>>(a, inv, w, T, topk + 1, h, h_stride);
     RLQ_HIP(hipGetLastError());
     return 0;
   }

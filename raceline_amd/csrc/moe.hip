@@ -76,63 +76,101 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
 }
 
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 // One wave per token. Lane l holds logits l, l + 64, ...; repeated wave-wide argmax with
 // ties to the lower expert (kernels/moe.metal:75-91). Weights: exp(l - max) over the
 // softmax denominator of all E logits, or over the chosen ones when norm_topk
 // (moe.metal:92-102); the shared slot gets sigmoid(logit[E]) (moe.metal:103-104).
-// A round takes the wave max of the lanes' best untaken logits, then the lowest expert
-// holding it: the first slot j whose ballot (logit == max, untaken) is not empty, and its
-// lowest lane. Every value of a round is wave-uniform; lane r keeps round r's pick.
+// Each lane first orders its EPL logits, highest first (equal ones by expert); a round
+// then takes the wave max of the lanes' first untaken logits, and the expert is the lowest
+// one among the lanes holding it: the only such lane's (one ballot bit, the usual case), or
+// a wave min of expert numbers. That lane drops its first entry. Entries past E and NaN
+// logits are -inf; an expert < E always wins a tie with them (topk <= E). Lane r keeps
+// round r's pick and logit; the exponentials are taken afterwards, one per lane, and
+// summed in round order.
 template <int EPL>
 __device__ void topk_token(const float *row, int E, int topk, int norm_topk, int *sel_t, float *w_t, int lane) {
+  const float shared_logit = row[E];
   float v[EPL];
+  int ev[EPL];
   float lm = -INFINITY;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
     const float l = e < E ? row[e] : -INFINITY;
     v[j] = l == l ? l : -INFINITY;            // a NaN logit ranks last
+    ev[j] = e;
     lm = fmaxf(lm, v[j]);
   }
+  asm volatile("" ::"s"(shared_logit));   // read beside the others, not after the rounds
   const float m = wave_max(lm);
-  float lz = 0.0f;
+  float z = 0.0f;
+  if (!norm_topk) {
+    float lz = 0.0f;
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) lz += (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
-  const float z = wave_sum(lz);
+    for (int j = 0; j < EPL; ++j) lz += (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
+    z = wave_sum(lz);
+  }
+  // highest first; a strictly higher logit moves ahead, so equal ones stay in expert order
+#pragma unroll
+  for (int i = 1; i < EPL; ++i)
+#pragma unroll
+    for (int j = i; j > 0; --j)
+      if (v[j] > v[j - 1]) {
+        const float tv = v[j];
+        v[j] = v[j - 1];
+        v[j - 1] = tv;
+        const int te = ev[j];
+        ev[j] = ev[j - 1];
+        ev[j - 1] = te;
+      }
 
-  // Chosen experts are tracked in `taken`, so every pick is a distinct expert < E even
-  // when logits tie at -inf (topk <= E guarantees a candidate).
-  uint32_t taken = 0;
   int my_which = 0;
-  float my_ex = 0.0f, sum = 0.0f;
+  float my_top = 0.0f;
   for (int r = 0; r < topk; ++r) {
-    float bv = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j)
-      if (lane + 64 * j < E && !((taken >> j) & 1u)) bv = fmaxf(bv, v[j]);
-    const float top = wave_max(bv);
-    int be = -1;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const uint64_t b = __ballot(lane + 64 * j < E && !((taken >> j) & 1u) && v[j] == top);
-      if (be < 0 && b != 0) be = 64 * j + __builtin_ctzll(b);
+    const float top = wave_max(v[0]);
+    const uint64_t b = __ballot(v[0] == top);
+    int be;
+    if (__popcll(b) == 1) {
+      be = __builtin_amdgcn_readlane(ev[0], (int)__builtin_ctzll(b));
+    } else {
+      be = wave_min_i(v[0] == top ? ev[0] : INT_MAX);
     }
-    if (be >= 0 && lane == (be & 63)) taken |= 1u << (be >> 6);
-    const float ex = expf(top - m);
-    sum += ex;
+    if (lane == (be & 63) && ev[0] == be) {
+#pragma unroll
+      for (int j = 0; j + 1 < EPL; ++j) {
+        v[j] = v[j + 1];
+        ev[j] = ev[j + 1];
+      }
+      v[EPL - 1] = -INFINITY;
+      ev[EPL - 1] = INT_MAX;
+    }
     if (lane == r) {
       my_which = be;
-      my_ex = ex;
+      my_top = top;
     }
   }
-  const float denom = norm_topk ? sum : z;
+  const float ex = lane < topk ? expf(my_top - m) : 0.0f;
+  float denom = z;
+  if (norm_topk) {
+    denom = 0.0f;
+    for (int r = 0; r < topk; ++r) denom += row_lane(ex, r);
+  }
   if (lane < topk) {
     sel_t[lane] = my_which;
-    w_t[lane] = my_ex / denom;
+    w_t[lane] = ex / denom;
   }
   if (lane == 0) {
     sel_t[topk] = E;
-    w_t[topk] = 1.0f / (1.0f + expf(-row[E]));
+    w_t[topk] = 1.0f / (1.0f + expf(-shared_logit));
   }
 }
 

@@ -87,6 +87,27 @@ def test_route(gpu, T, E, topk, norm):
         np.testing.assert_array_equal(np.sort(inv[sel_ref == e]), np.arange(off[e], off[e + 1]))
 
 
+@pytest.mark.parametrize("T,E,topk,norm", [(1, 256, 8, True), (3, 256, 8, False), (33, 64, 8, True),
+                                           (20, 16, 16, True), (5, 700, 16, True)])
+def test_route_many_ties(gpu, T, E, topk, norm):
+    """Logits that tie a lot: small integers, one row all equal, one row with only three
+    finite logits (the rest -inf, so the picks run into the -inf ties). The chosen experts
+    follow the stable order: equal logits by expert number."""
+    from raceline_amd import ops
+
+    rng = np.random.default_rng(T * 11 + E)
+    logits = rng.integers(-2, 3, size=(T, E + 1)).astype(np.float32)
+    logits[0, :E] = 0.5
+    if T > 1:
+        logits[1, :E] = -np.inf
+        logits[1, [E - 1, E // 2, 3]] = [1.0, 1.0, -1.0]
+    r = ops.moe_route(to_dev(logits, gpu), E, topk, norm)
+    _sync()
+    sel_ref, w_ref = O.moe_route(logits, E, topk, norm)
+    np.testing.assert_array_equal(r.sel.cpu().numpy(), sel_ref)
+    np.testing.assert_allclose(r.w.cpu().numpy(), w_ref, rtol=1e-6, atol=1e-7)
+
+
 @pytest.mark.parametrize("sd", ["f16", "bf16"])
 def test_gate_up_swiglu_and_down(gpu, sd):
     from raceline_amd import ops

@@ -300,12 +300,13 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
 }
 
 // Several tokens, two adjacent tiles per workgroup (t0 = 2 * block, t1 = t0 + 1): each wave
-// reads its activation operands once for both tiles (tile_dot_rows2). At M > 1 the
+// reads its activation operands once for both tiles (tile_dot_rows2_staged). At M > 1 the
 // activations are a wave's largest stream (a group's operands are M * 128 bytes against
 // the 576 bytes of one tile's codes and scales, and they come from L2 once per tile), so
-// pairing halves it. Taken where a wave holds 8 groups: two tiles' loads then fit the
-// registers one tile of 16 groups takes. Each tile's sums are the one-tile kernel's, in
-// the same order, so the results do not depend on the pairing.
+// pairing halves it; and they are staged in LDS by DMA together with the weight loads, so
+// no group waits on an L2 read. Taken where a wave holds 8 groups: two tiles' loads then
+// fit the registers one tile of 16 groups takes. Each tile's sums are the one-tile
+// kernel's, in the same order, so the results do not depend on the pairing.
 template <int GPW, int SD, bool ACC, int BOOK>
 __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -317,7 +318,6 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
   const int tiles = tiles_of(a.N);
   const int t0 = 2 * blockIdx.x, t1 = t0 + 1;
   const int M = a.M;
-  f32x4 *red = reinterpret_cast<f32x4 *>(lds);   // [2][waves-1][64]
 
   const int wg0 = wave * GPW;
   const int wn = max(0, min(G, wg0 + GPW) - wg0);
@@ -325,19 +325,22 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
   const WaveTile w1 = wave_tile(a.codes, a.sb, min(t1, tiles - 1), G4, wg0, t1 < tiles ? GPW : 0);
   const uint32_t xrange = wn > 0 ? (uint32_t)((M - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
+  // LDS: wave w's staged activation rows at w * M * kStagedXRow; once the wave is done with
+  // them, its two partials (2 x 64 f32x4 <= 2 rows) take their place
+  unsigned char *xs = lds + (size_t)wave * M * kStagedXRow;
   f32x4 acc0, acc1;
-  tile_dot_rows2<GPW, SD, BOOK>(w0, w1, rx, (uint32_t)c16 * a.x_stride * 2u + 16u * j4, c16 < M, wn, lane, acc0,
-                                acc1);
+  tile_dot_rows2_staged<GPW, SD, BOOK>(w0, w1, rx, (uint32_t)a.x_stride * 2u, M, xs, wn, lane, acc0, acc1);
 
   // the waves' partials meet in wave order, as in reduce_waves
   if (wave > 0) {
-    red[(wave - 1) * 64 + lane] = acc0;
-    red[(waves - 1 + wave - 1) * 64 + lane] = acc1;
+    reinterpret_cast<f32x4 *>(xs)[lane] = acc0;
+    reinterpret_cast<f32x4 *>(xs)[64 + lane] = acc1;
   }
   __syncthreads();
   if (wave != 0 || 4 * j4 >= M) return;
   for (int w = 1; w < waves; ++w) {
-    const f32x4 o0 = red[(w - 1) * 64 + lane], o1 = red[(waves - 1 + w - 1) * 64 + lane];
+    const f32x4 *red = reinterpret_cast<const f32x4 *>(lds + (size_t)w * M * kStagedXRow);
+    const f32x4 o0 = red[lane], o1 = red[64 + lane];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       acc0[v] += o0[v];
@@ -424,8 +427,9 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
                    : gpw == 12 ? launch_gemv<1, 12>(book, sd, accum, grid, threads, lds, st, a)
                    : gpw == 16 ? launch_gemv<1, 16>(book, sd, accum, grid, threads, lds, st, a)
                                : launch_gemv<1, 24>(book, sd, accum, grid, threads, lds, st, a);
-  else if (gpw == 8)   // two tiles per workgroup
-    rc = launch_gemv<kGemvMaxM, 8, true>(book, sd, accum, dim3((tiles_of(N) + 1) / 2), threads, 2 * lds, st, a);
+  else if (gpw == 8)   // two tiles per workgroup, activations staged in LDS
+    rc = launch_gemv<kGemvMaxM, 8, true>(book, sd, accum, dim3((tiles_of(N) + 1) / 2), threads,
+                                         (size_t)waves * M * kStagedXRow, st, a);
   else rc = gpw == 12 ? launch_gemv<kGemvMaxM, 12>(book, sd, accum, grid, threads, lds, st, a)
             : gpw == 16 ? launch_gemv<kGemvMaxM, 16>(book, sd, accum, grid, threads, lds, st, a)
                         : launch_gemv<kGemvMaxM, 24>(book, sd, accum, grid, threads, lds, st, a);

@@ -305,6 +305,82 @@ __device__ __forceinline__ void tile_dot_rows2(const WaveTile &w0, const WaveTil
   }
 }
 
+// LDS bytes of one staged activation row of an 8-group wave range (tile_dot_rows2_staged):
+// the range's 1024 bytes and 16 of padding, so the 16 rows a wave reads at once start in
+// different banks.
+constexpr int kStagedXRow = 8 * kGroup * 2 + 16;
+
+// tile_dot_rows2 with the activations staged in LDS first: one LDS-DMA per token row
+// (lane l brings bytes 16 l .. 16 l + 15 of the row's part of the wave's range, with no
+// registers or ALU work), issued before the weight loads, so the activations and the
+// weights are in flight together and the groups then read their operands from LDS
+// instead of waiting on L2 reads one or two groups ahead. xs: the wave's M * kStagedXRow
+// bytes; xstride: bytes between token rows in memory. Rows >= M and groups >= wn use zero
+// operands, as tile_dot_rows2's zero reads give, so acc0 and acc1 hold its bits.
+// GPW = 8 only (a row's part is one 1024-byte LDS-DMA).
+template <int GPW, int SD, int BOOK = kAffine>
+__device__ __forceinline__ void tile_dot_rows2_staged(const WaveTile &w0, const WaveTile &w1,
+                                                      __amdgpu_buffer_rsrc_t rx, uint32_t xstride, int M,
+                                                      unsigned char *xs, int wn, int lane, f32x4 &acc0,
+                                                      f32x4 &acc1) {
+  static_assert(GPW == 8, "one 1024-byte LDS-DMA per activation row");
+  u32x4 wq0[GPW / 2], sq0[GPW / 4], wq1[GPW / 2], sq1[GPW / 4];
+  for (int r = 0; r < M; ++r)   // uniform
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void *)(xs + r * kStagedXRow), 16,
+                                             (uint32_t)r * xstride + 16u * lane, 0, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);   // the activations are requested first: they complete first
+  issue_tile_loads<GPW, BOOK>(w0, lane, wq0, sq0);
+  issue_tile_loads<GPW, BOOK>(w1, lane, wq1, sq1);
+  // the activation DMAs have landed once at most the weight loads are outstanding
+  constexpr int kWeightLoads = 2 * (GPW / 2 + (BOOK == kAffine ? GPW / 4 : 0));
+  __builtin_amdgcn_s_waitcnt(0x0F70 | kWeightLoads);   // vmcnt(kWeightLoads); expcnt, lgkmcnt: no wait
+  __builtin_amdgcn_sched_barrier(0);
+  const bool live = (lane & 15) < M;
+  const unsigned char *xa = xs + (live ? lane & 15 : 0) * kStagedXRow + 16 * (lane >> 4);
+  auto ldx = [&](int jg, int s) -> u32x4 {
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(xa + jg * kGroup * 2 + 64 * s);
+    return live && jg < wn ? v : u32x4{};
+  };
+  const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
+  f32x4 asum = {};
+  acc0 = f32x4{};
+  acc1 = f32x4{};
+  u32x4 ax[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) ax[0][s] = ldx(0, s);
+#pragma unroll
+  for (int jg = 0; jg < GPW; ++jg) {
+    if (jg + 1 < GPW) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) ax[(jg + 1) & 1][s] = ldx(jg + 1, s);
+    }
+    const half8 af[2] = {__builtin_bit_cast(half8, prep_act<BOOK>(ax[jg & 1][0])),
+                         __builtin_bit_cast(half8, prep_act<BOOK>(ax[jg & 1][1]))};
+    if constexpr (BOOK == kAffine) {
+      const f32x4 gsv = group_sums(af);
+      group_step_gs<GPW, SD, 4>(acc0, af, gsv, wq0, sq0, jg);
+      group_step_gs<GPW, SD, 4>(acc1, af, gsv, wq1, sq1, jg);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq0[jg >> 1][2 * (jg & 1) + s]),
+                                                      acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq1[jg >> 1][2 * (jg & 1) + s]),
+                                                      acc1, 0, 0, 0);
+        if constexpr (BOOK == kInt16) asum = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, asum, 0, 0, 0);
+      }
+    }
+    asm volatile("" : "+v"(acc0), "+v"(acc1));   // each group's epilogue stays with its group
+  }
+  if constexpr (BOOK == kInt16) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      acc0[v] = __builtin_fmaf(0.5f, asum[v], acc0[v]);
+      acc1[v] = __builtin_fmaf(0.5f, asum[v], acc1[v]);
+    }
+  }
+}
+
 // The wave's part of a 16-row affine weight tile (its loads already issued into wq, sq)
 // times 16 token rows staged in LDS in operand order, with their group sums formed
 // beforehand (group_sums): xs points at row 0's element 64 * wg0 (the wave's first group),

@@ -203,10 +203,12 @@ static int gemv_gpw(int K) {
 }
 static int gemv_waves(int K) { const int g = gemv_gpw(K); return (4 * quads_of(K) + g - 1) / g; }
 
-// the cross-wave reduction [waves-1][64][4] floats, then (M = 1) each wave's staged
-// activations [gpw * 64] halves
+// M = 1: the cross-wave reduction [waves-1][64][4] floats, then each wave's staged
+// activations [gpw * 64] halves. M > 1: each wave's staged rows, M * kStagedXRow bytes
+// (its partial takes their place for the reduction).
 static size_t gemv_lds_bytes(int M, int waves, int gpw) {
-  return (size_t)(waves - 1) * 64 * 16 + (M == 1 ? (size_t)waves * gpw * kGroup * 2 : 0);
+  if (M > 1) return (size_t)waves * M * kStagedXRow;
+  return (size_t)(waves - 1) * 64 * 16 + (size_t)waves * gpw * kGroup * 2;
 }
 
 // MAXM: 1 (single-token decode: one activation row, one live accumulator) or 8.
@@ -278,13 +280,24 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
     }
     if constexpr (BOOK == kInt16) acc[0] = __builtin_fmaf(0.5f, asum[0], acc[0]);
   } else {
-    // Several tokens: lane (c16, j4) reads token row c16's activations from memory;
-    // rows >= M read zeros.
-    acc = tile_dot_rows<GPW, SD, BOOK>(wt, rx, (uint32_t)c16 * a.x_stride * 2u + 16u * j4, c16 < M, wn, lane);
+    // Several tokens: the wave's rows are staged in LDS 8 groups at a time (its
+    // M * kStagedXRow bytes at wave * M * kStagedXRow); lane (c16, j4) multiplies token
+    // row c16, rows >= M are zeros.
+    unsigned char *xs = lds + (size_t)wave * M * kStagedXRow;
+    acc = tile_dot_rows_staged<GPW, SD, BOOK>(wt, rx, (uint32_t)a.x_stride * 2u, M, xs, wn, lane);
+    // the partials meet in wave order, as in reduce_waves, each in its wave's staging bytes
+    if (wave > 0) reinterpret_cast<f32x4 *>(xs)[lane] = acc;
+    __syncthreads();
+    if (wave == 0)
+      for (int w = 1; w < waves; ++w) {
+        const f32x4 o = reinterpret_cast<const f32x4 *>(lds + (size_t)w * M * kStagedXRow)[lane];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] += o[v];
+      }
   }
 
   // lane (c16, j4) holds token rows 4 j4 .. 4 j4 + 3 of output n
-  acc = reduce_waves(acc, red, wave, waves, lane);
+  if constexpr (MAXM == 1) acc = reduce_waves(acc, red, wave, waves, lane);
   if (wave == 0 && n < a.N && 4 * j4 < M) {
     const float rs = BOOK == kAffine ? 1.0f : a.srow[n];
 #pragma unroll
@@ -428,8 +441,7 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
                    : gpw == 16 ? launch_gemv<1, 16>(book, sd, accum, grid, threads, lds, st, a)
                                : launch_gemv<1, 24>(book, sd, accum, grid, threads, lds, st, a);
   else if (gpw == 8)   // two tiles per workgroup, activations staged in LDS
-    rc = launch_gemv<kGemvMaxM, 8, true>(book, sd, accum, dim3((tiles_of(N) + 1) / 2), threads,
-                                         (size_t)waves * M * kStagedXRow, st, a);
+    rc = launch_gemv<kGemvMaxM, 8, true>(book, sd, accum, dim3((tiles_of(N) + 1) / 2), threads, lds, st, a);
   else rc = gpw == 12 ? launch_gemv<kGemvMaxM, 12>(book, sd, accum, grid, threads, lds, st, a)
             : gpw == 16 ? launch_gemv<kGemvMaxM, 16>(book, sd, accum, grid, threads, lds, st, a)
                         : launch_gemv<kGemvMaxM, 24>(book, sd, accum, grid, threads, lds, st, a);

@@ -310,6 +310,10 @@ __device__ __forceinline__ void tile_dot_rows2(const WaveTile &w0, const WaveTil
 // different banks.
 constexpr int kStagedXRow = 8 * kGroup * 2 + 16;
 
+// s_waitcnt immediate that waits until at most n vector memory operations are outstanding
+// (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt at their no-wait maximum).
+constexpr int waitcnt_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+
 // tile_dot_rows2 with the activations staged in LDS first: one LDS-DMA per token row
 // (lane l brings bytes 16 l .. 16 l + 15 of the row's part of the wave's range, with no
 // registers or ALU work), issued before the weight loads, so the activations and the
@@ -333,7 +337,7 @@ __device__ __forceinline__ void tile_dot_rows2_staged(const WaveTile &w0, const 
   issue_tile_loads<GPW, BOOK>(w1, lane, wq1, sq1);
   // the activation DMAs have landed once at most the weight loads are outstanding
   constexpr int kWeightLoads = 2 * (GPW / 2 + (BOOK == kAffine ? GPW / 4 : 0));
-  __builtin_amdgcn_s_waitcnt(0x0F70 | kWeightLoads);   // vmcnt(kWeightLoads); expcnt, lgkmcnt: no wait
+  __builtin_amdgcn_s_waitcnt(waitcnt_vmcnt(kWeightLoads));
   __builtin_amdgcn_sched_barrier(0);
   const bool live = (lane & 15) < M;
   const unsigned char *xa = xs + (live ? lane & 15 : 0) * kStagedXRow + 16 * (lane >> 4);
@@ -379,6 +383,69 @@ __device__ __forceinline__ void tile_dot_rows2_staged(const WaveTile &w0, const 
       acc1[v] = __builtin_fmaf(0.5f, asum[v], acc1[v]);
     }
   }
+}
+
+// tile_dot_rows with the activations staged in LDS by DMA, 8 groups at a time (a row's
+// part of a chunk is one 1024-byte LDS-DMA, lane l bringing bytes 16 l .. 16 l + 15), for
+// wave ranges too long for all their rows to sit in LDS at once (12, 16 or 24 groups: the
+// down projections). Chunk 0 is requested before the weight loads, so it arrives with
+// them; each later chunk replaces the previous one in the wave's M * kStagedXRow bytes at
+// xs once its groups are done. Rows >= M and groups >= wn use zero operands, as
+// tile_dot_rows's zero reads give, so the result holds its bits.
+template <int GPW, int SD, int BOOK = kAffine>
+__device__ __forceinline__ f32x4 tile_dot_rows_staged(const WaveTile &w, __amdgpu_buffer_rsrc_t rx, uint32_t xstride,
+                                                      int M, unsigned char *xs, int wn, int lane) {
+  static_assert(GPW % 4 == 0, "chunks of 8 groups, the last possibly 4");
+  u32x4 wq[GPW / 2], sq[GPW / 4];
+  auto stage = [&](int chunk) {
+    for (int r = 0; r < M; ++r)   // uniform
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void *)(xs + r * kStagedXRow), 16,
+          (uint32_t)r * xstride + (uint32_t)chunk * 8u * kGroup * 2u + 16u * lane, 0, 0, 0);
+  };
+  stage(0);
+  __builtin_amdgcn_sched_barrier(0);   // chunk 0 is requested first: it completes first
+  issue_tile_loads<GPW, BOOK>(w, lane, wq, sq);
+  constexpr int kWeightLoads = GPW / 2 + (BOOK == kAffine ? GPW / 4 : 0);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vmcnt(kWeightLoads));   // chunk 0 has landed
+  __builtin_amdgcn_sched_barrier(0);
+  const bool live = (lane & 15) < M;
+  const unsigned char *xa = xs + (live ? lane & 15 : 0) * kStagedXRow + 16 * (lane >> 4);
+  auto ldx = [&](int jg, int s) -> u32x4 {
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(xa + (jg & 7) * kGroup * 2 + 64 * s);
+    return live && jg < wn ? v : u32x4{};
+  };
+  f32x4 acc = {}, asum = {};
+  u32x4 ax[2][2];
+#pragma unroll
+  for (int jg = 0; jg < GPW; ++jg) {
+    if ((jg & 7) == 0) {
+      if (jg > 0) {
+        // the previous chunk's operands are in registers (its reads have returned); bring
+        // the next chunk into the same bytes and wait for it
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt: no wait
+        __builtin_amdgcn_sched_barrier(0);
+        stage(jg / 8);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vmcnt(0));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) ax[jg & 1][s] = ldx(jg, s);
+    }
+    if (((jg + 1) & 7) != 0 && jg + 1 < GPW) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) ax[(jg + 1) & 1][s] = ldx(jg + 1, s);
+    }
+    const half8 af[2] = {__builtin_bit_cast(half8, prep_act<BOOK>(ax[jg & 1][0])),
+                         __builtin_bit_cast(half8, prep_act<BOOK>(ax[jg & 1][1]))};
+    book_step<GPW, SD, 4, BOOK>(acc, asum, af, wq, sq, jg);
+    asm volatile("" : "+v"(acc));   // each group's epilogue stays with its group
+  }
+  if constexpr (BOOK == kInt16) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(0.5f, asum[v], acc[v]);
+  }
+  return acc;
 }
 
 // The wave's part of a 16-row affine weight tile (its loads already issued into wq, sq)

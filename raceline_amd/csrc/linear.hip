@@ -284,7 +284,8 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
     // M * kStagedXRow bytes at wave * M * kStagedXRow); lane (c16, j4) multiplies token
     // row c16, rows >= M are zeros.
     unsigned char *xs = lds + (size_t)wave * M * kStagedXRow;
-    acc = tile_dot_rows_staged<GPW, SD, BOOK>(wt, rx, (uint32_t)a.x_stride * 2u, M, xs, wn, lane);
+    const uint32_t xstride = (uint32_t)a.x_stride * 2u;
+    acc = tile_dot_rows_staged<GPW, SD, BOOK>(wt, rx, [=](int r) { return (uint32_t)r * xstride; }, M, xs, wn, lane);
     // the partials meet in wave order, as in reduce_waves, each in its wave's staging bytes
     if (wave > 0) reinterpret_cast<f32x4 *>(xs)[lane] = acc;
     __syncthreads();

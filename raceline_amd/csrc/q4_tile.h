@@ -385,25 +385,34 @@ __device__ __forceinline__ void tile_dot_rows2_staged(const WaveTile &w0, const 
   }
 }
 
-// tile_dot_rows with the activations staged in LDS by DMA, 8 groups at a time (a row's
-// part of a chunk is one 1024-byte LDS-DMA, lane l bringing bytes 16 l .. 16 l + 15), for
-// wave ranges too long for all their rows to sit in LDS at once (12, 16 or 24 groups: the
-// down projections). Chunk 0 is requested before the weight loads, so it arrives with
-// them; each later chunk replaces the previous one in the wave's M * kStagedXRow bytes at
-// xs once its groups are done. Rows >= M and groups >= wn use zero operands, as
-// tile_dot_rows's zero reads give, so the result holds its bits.
-template <int GPW, int SD, int BOOK = kAffine>
-__device__ __forceinline__ f32x4 tile_dot_rows_staged(const WaveTile &w, __amdgpu_buffer_rsrc_t rx, uint32_t xstride,
-                                                      int M, unsigned char *xs, int wn, int lane) {
+// Requests chunk `chunk` (groups 8 chunk .. 8 chunk + 7 of the wave's range) of M token
+// rows into LDS: row r's 1024 bytes, from byte offset row_off(r) (uniform) of rx, land at
+// xs + r * kStagedXRow, lane l bringing bytes 16 l .. 16 l + 15 (one LDS-DMA per row, no
+// registers or ALU work; bytes past rx's range read as zero).
+template <typename RowOff>
+__device__ __forceinline__ void stage_rows(__amdgpu_buffer_rsrc_t rx, RowOff row_off, int M, int chunk,
+                                           unsigned char *xs, int lane) {
+  for (int r = 0; r < M; ++r)   // uniform
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void *)(xs + r * kStagedXRow), 16,
+                                             row_off(r) + (uint32_t)chunk * 8u * kGroup * 2u + 16u * lane, 0, 0, 0);
+}
+
+// tile_dot_rows with the activations staged in LDS by DMA (stage_rows), 8 groups at a
+// time, for any wave range (the down projections' 12, 16 or 24 groups do not fit LDS whole
+// for every row). Chunk 0 is requested before the weight loads, so it arrives with them
+// (or, staged0, the caller requested it earlier, before any other vector memory load of
+// the wave still in flight); each later chunk replaces the previous one in the wave's
+// M * kStagedXRow bytes at xs once its groups are done. Row r comes from byte offset
+// row_off(r) of rx. Rows >= M and groups >= wn use zero operands, as tile_dot_rows's zero
+// reads give, so the result holds its bits.
+template <int GPW, int SD, int BOOK = kAffine, typename RowOff>
+__device__ __forceinline__ f32x4 tile_dot_rows_staged(const WaveTile &w, __amdgpu_buffer_rsrc_t rx, RowOff row_off,
+                                                      int M, unsigned char *xs, int wn, int lane,
+                                                      bool staged0 = false) {
   static_assert(GPW % 4 == 0, "chunks of 8 groups, the last possibly 4");
   u32x4 wq[GPW / 2], sq[GPW / 4];
-  auto stage = [&](int chunk) {
-    for (int r = 0; r < M; ++r)   // uniform
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (__attribute__((address_space(3))) void *)(xs + r * kStagedXRow), 16,
-          (uint32_t)r * xstride + (uint32_t)chunk * 8u * kGroup * 2u + 16u * lane, 0, 0, 0);
-  };
-  stage(0);
+  auto stage = [&](int chunk) { stage_rows(rx, row_off, M, chunk, xs, lane); };
+  if (!staged0) stage(0);
   __builtin_amdgcn_sched_barrier(0);   // chunk 0 is requested first: it completes first
   issue_tile_loads<GPW, BOOK>(w, lane, wq, sq);
   constexpr int kWeightLoads = GPW / 2 + (BOOK == kAffine ? GPW / 4 : 0);

@@ -305,18 +305,19 @@ __device__ __forceinline__ void tile_dot_rows2(const WaveTile &w0, const WaveTil
   }
 }
 
-// LDS bytes of one staged activation row of an 8-group wave range (tile_dot_rows2_staged):
-// the range's 1024 bytes and 16 of padding, so the 16 rows a wave reads at once start in
-// different banks.
-constexpr int kStagedXRow = 8 * kGroup * 2 + 16;
+// LDS bytes of one staged activation row of an 8-group wave range: its 64 chunks of 16
+// bytes, chunk c of row r at position c ^ (r & 15), so the 16 rows a wave reads at once
+// (the same chunk of each) fall in different banks without padding.
+constexpr int kStagedXRow = 8 * kGroup * 2;
+__device__ __forceinline__ int staged_pos(int c, int r) { return c ^ (r & 15); }
 
 // s_waitcnt immediate that waits until at most n vector memory operations are outstanding
 // (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt at their no-wait maximum).
 constexpr int waitcnt_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
 // tile_dot_rows2 with the activations staged in LDS first: one LDS-DMA per token row
-// (lane l brings bytes 16 l .. 16 l + 15 of the row's part of the wave's range, with no
-// registers or ALU work), issued before the weight loads, so the activations and the
+// (stage_rows: the row's part of the wave's range, with no registers or ALU work), issued
+// before the weight loads, so the activations and the
 // weights are in flight together and the groups then read their operands from LDS
 // instead of waiting on L2 reads one or two groups ahead. xs: the wave's M * kStagedXRow
 // bytes; xstride: bytes between token rows in memory. Rows >= M and groups >= wn use zero
@@ -329,9 +330,7 @@ __device__ __forceinline__ void tile_dot_rows2_staged(const WaveTile &w0, const 
                                                       f32x4 &acc1) {
   static_assert(GPW == 8, "one 1024-byte LDS-DMA per activation row");
   u32x4 wq0[GPW / 2], sq0[GPW / 4], wq1[GPW / 2], sq1[GPW / 4];
-  for (int r = 0; r < M; ++r)   // uniform
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void *)(xs + r * kStagedXRow), 16,
-                                             (uint32_t)r * xstride + 16u * lane, 0, 0, 0);
+  stage_rows(rx, [=](int r) { return (uint32_t)r * xstride; }, M, 0, xs, lane);
   __builtin_amdgcn_sched_barrier(0);   // the activations are requested first: they complete first
   issue_tile_loads<GPW, BOOK>(w0, lane, wq0, sq0);
   issue_tile_loads<GPW, BOOK>(w1, lane, wq1, sq1);
@@ -340,9 +339,14 @@ __device__ __forceinline__ void tile_dot_rows2_staged(const WaveTile &w0, const 
   __builtin_amdgcn_s_waitcnt(waitcnt_vmcnt(kWeightLoads));
   __builtin_amdgcn_sched_barrier(0);
   const bool live = (lane & 15) < M;
-  const unsigned char *xa = xs + (live ? lane & 15 : 0) * kStagedXRow + 16 * (lane >> 4);
+  const int row = live ? lane & 15 : 0;
+  // chunk 8 jg + 4 s + j4 of the lane's row: the swizzle only moves it inside its 256-byte
+  // block, so four per-lane bases (jg odd or even, s) and a constant offset reach every one
+  const unsigned char *xq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) xq[q] = xs + row * kStagedXRow + 16 * staged_pos(8 * (q >> 1) + 4 * (q & 1) + (lane >> 4), row);
   auto ldx = [&](int jg, int s) -> u32x4 {
-    const u32x4 v = *reinterpret_cast<const u32x4 *>(xa + jg * kGroup * 2 + 64 * s);
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(xq[2 * (jg & 1) + s] + 256 * (jg >> 1));
     return live && jg < wn ? v : u32x4{};
   };
   const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
@@ -387,14 +391,16 @@ __device__ __forceinline__ void tile_dot_rows2_staged(const WaveTile &w0, const 
 
 // Requests chunk `chunk` (groups 8 chunk .. 8 chunk + 7 of the wave's range) of M token
 // rows into LDS: row r's 1024 bytes, from byte offset row_off(r) (uniform) of rx, land at
-// xs + r * kStagedXRow, lane l bringing bytes 16 l .. 16 l + 15 (one LDS-DMA per row, no
-// registers or ALU work; bytes past rx's range read as zero).
+// xs + r * kStagedXRow in staged_pos order (one LDS-DMA per row, no registers or ALU work:
+// lane l fills position l, so it brings source chunk staged_pos(l, r)); bytes past rx's
+// range read as zero.
 template <typename RowOff>
 __device__ __forceinline__ void stage_rows(__amdgpu_buffer_rsrc_t rx, RowOff row_off, int M, int chunk,
                                            unsigned char *xs, int lane) {
   for (int r = 0; r < M; ++r)   // uniform
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void *)(xs + r * kStagedXRow), 16,
-                                             row_off(r) + (uint32_t)chunk * 8u * kGroup * 2u + 16u * lane, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rx, (__attribute__((address_space(3))) void *)(xs + r * kStagedXRow), 16,
+        row_off(r) + (uint32_t)chunk * 8u * kGroup * 2u + 16u * (uint32_t)staged_pos(lane, r), 0, 0, 0);
 }
 
 // tile_dot_rows with the activations staged in LDS by DMA (stage_rows), 8 groups at a
@@ -419,9 +425,13 @@ __device__ __forceinline__ f32x4 tile_dot_rows_staged(const WaveTile &w, __amdgp
   __builtin_amdgcn_s_waitcnt(waitcnt_vmcnt(kWeightLoads));   // chunk 0 has landed
   __builtin_amdgcn_sched_barrier(0);
   const bool live = (lane & 15) < M;
-  const unsigned char *xa = xs + (live ? lane & 15 : 0) * kStagedXRow + 16 * (lane >> 4);
+  const int row = live ? lane & 15 : 0;
+  // chunk 8 (jg % 8) + 4 s + j4 of the lane's row, reached as in tile_dot_rows2_staged
+  const unsigned char *xq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) xq[q] = xs + row * kStagedXRow + 16 * staged_pos(8 * (q >> 1) + 4 * (q & 1) + (lane >> 4), row);
   auto ldx = [&](int jg, int s) -> u32x4 {
-    const u32x4 v = *reinterpret_cast<const u32x4 *>(xa + (jg & 7) * kGroup * 2 + 64 * s);
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(xq[2 * (jg & 1) + s] + 256 * ((jg & 7) >> 1));
     return live && jg < wn ? v : u32x4{};
   };
   f32x4 acc = {}, asum = {};

@@ -60,6 +60,9 @@ GEMV_CASES = [  # (M, K, N); the decode kernel takes M <= 8
     (8, 512, 2048), (8, 1024, 300), (7, 640, 96), (1, 17408, 640), (4, 64, 33), (1, 12288, 4096),
     (5, 4096, 6144),  # the 9B layer's stacked q/k/v
     (1, 64, 16), (3, 320, 40), (8, 576, 17),  # one group; odd group counts
+    # several tokens over 12, 16 and 24 groups per wave (activation rows staged 8 groups at
+    # a time; the last wave's range ends inside its second chunk or holds one group of it)
+    (6, 13312, 200), (2, 8256, 64), (8, 17408, 48),
 ]
 
 
@@ -110,10 +113,11 @@ def test_gemm_accumulates(gpu, M, K, N):
     O.check_close(y, O.linear_affine_f64(x, q, s, b) + y0, TOL, "gemm accum")
 
 
-def test_rows_do_not_depend_on_other_rows(gpu):
+@pytest.mark.parametrize("K", [4096, 9216, 17408])   # two tiles per workgroup; 12 and 24 groups per wave
+def test_rows_do_not_depend_on_other_rows(gpu, K):
     """A token's result is bit-identical whatever rows share the call (the reference's
     determinism rule, kernels/linear.metal:264-266): one row alone vs. inside M = 8."""
-    M, K, N = 8, 4096, 1024
+    M, N = 8, 1024
     q, s, b = make_layer(11, N, K)
     x = make_x(12, M, K)
     wt = upload(q, s, b, "f16", gpu)

@@ -177,10 +177,11 @@ __global__ void dequant_kernel(const u32x4 *codes, const u32x4 *sb, int K, int N
 // non-temporally (they are used once).
 //
 // One token (M = 1): each wave stages its activation range in LDS, in operand order.
-// Several tokens: lanes read their activation operands straight from memory (L2-resident,
-// shared by every workgroup) and reorder them in registers. Either way the group sums
-// come from an MFMA against a constant operand, which lands them in the accumulator
-// layout, and every weight load of a wave is issued before its first multiply.
+// Several tokens: each wave has its token rows brought into LDS by DMA (8 groups at a
+// time for ranges longer than 8 groups; L2-resident, shared by every workgroup) and
+// reorders each operand in registers as it reads it. Either way the group sums come from
+// an MFMA against a constant operand, which lands them in the accumulator layout, and
+// every weight load of a wave is issued before its first multiply.
 //
 // The operand trick and the MFMA group sums are described in q4_tile.h.
 constexpr int kGemvMaxM = 8;

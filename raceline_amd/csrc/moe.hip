@@ -238,10 +238,21 @@ __device__ void sort_assignments(const int *sel, int T, int E, int S, int wpe, i
 
   cnt[tid] = 0;
   run[tid] = 0;
-  __syncthreads();
   // sel comes from moe_topk_kernel (0 <= sel < E + 1); the clamps keep every index in
-  // range whatever it holds
-  for (int a = tid; a < A; a += 1024) atomicAdd(&cnt[min(max(sel[a], 0), E)], 1);
+  // range whatever it holds. The first kSortCached assignments of each thread stay in
+  // registers for the later passes (the one-chunk case: all of them up to A = 8192).
+  constexpr int kSortCached = 8;
+  int sv[kSortCached];
+#pragma unroll
+  for (int i = 0; i < kSortCached; ++i) {
+    const int a = tid + 1024 * i;
+    sv[i] = a < A ? min(max(sel[a], 0), E) : 0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kSortCached; ++i)
+    if (tid + 1024 * i < A) atomicAdd(&cnt[sv[i]], 1);
+  for (int a = tid + 1024 * kSortCached; a < A; a += 1024) atomicAdd(&cnt[min(max(sel[a], 0), E)], 1);
   __syncthreads();
   const int c = tid < E1 ? cnt[tid] : 0;
   const int ni = (c + kItemRows - 1) / kItemRows;
@@ -265,34 +276,54 @@ __device__ void sort_assignments(const int *sel, int T, int E, int S, int wpe, i
   __syncthreads();
 
   const int chunk = 32 * wpe;                   // tokens per chunk
+  // an assignment's expert: from registers in the one-chunk case (chunk 0 starts at a = 0,
+  // so the k-th assignment a thread visits is its k-th cached one), else from memory
+  const bool cached = T <= chunk && A <= 1024 * kSortCached;   // uniform
+  auto expert_of = [&](int a, int k) {
+    int e = 0;
+#pragma unroll
+    for (int i = 0; i < kSortCached; ++i) e = i == k ? sv[i] : e;
+    return cached ? e : min(max(sel[a], 0), E);
+  };
   for (int t0 = 0; t0 < T; t0 += chunk) {
     const int tn = min(chunk, T - t0);
+    const int nw = (tn + 31) / 32;              // bitmap words in use per expert
     for (int i = tid; i < E1 * wpe; i += 1024) bm[i] = 0u;
     __syncthreads();
-    for (int a = t0 * S + tid; a < (t0 + tn) * S; a += 1024) {
+    for (int a = t0 * S + tid, k = 0; a < (t0 + tn) * S; a += 1024, ++k) {
       const int tl = a / S - t0;
-      atomicOr(&bm[(size_t)min(max(sel[a], 0), E) * wpe + (tl >> 5)], 1u << (tl & 31));
+      atomicOr(&bm[(size_t)expert_of(a, k) * wpe + (tl >> 5)], 1u << (tl & 31));
     }
     __syncthreads();
     if (tid < E1) {
+      // running popcounts over the expert's words, eight words read at a time
       uint32_t acc = 0;
-      for (int i = 0; i < wpe; ++i) {
-        pre[(size_t)tid * wpe + i] = acc;
-        acc += __popc(bm[(size_t)tid * wpe + i]);
+      for (int i0 = 0; i0 < nw; i0 += 8) {
+        uint32_t wv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wv[i] = i0 + i < nw ? bm[(size_t)tid * wpe + i0 + i] : 0u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (i0 + i < nw) pre[(size_t)tid * wpe + i0 + i] = acc;
+          acc += __popc(wv[i]);
+        }
       }
     }
     __syncthreads();
-    for (int a = t0 * S + tid; a < (t0 + tn) * S; a += 1024) {
-      const int t = a / S, tl = t - t0, e = min(max(sel[a], 0), E);
+    for (int a = t0 * S + tid, k = 0; a < (t0 + tn) * S; a += 1024, ++k) {
+      const int t = a / S, tl = t - t0, e = expert_of(a, k);
       const size_t wi = (size_t)e * wpe + (tl >> 5);
       const int rank = run[e] + (int)pre[wi] + __popc(bm[wi] & ((1u << (tl & 31)) - 1u));
       const int pos = off[e] + rank;
       inv[a] = pos;
       tok[pos] = t;
     }
-    __syncthreads();
-    if (tid < E1) run[tid] += (int)(pre[(size_t)tid * wpe + wpe - 1] + __popc(bm[(size_t)tid * wpe + wpe - 1]));
-    __syncthreads();
+    if (t0 + chunk < T) {   // uniform: a later chunk continues each expert's rows
+      __syncthreads();
+      if (tid < E1)
+        run[tid] += (int)(pre[(size_t)tid * wpe + nw - 1] + __popc(bm[(size_t)tid * wpe + nw - 1]));
+      __syncthreads();
+    }
   }
 }
 

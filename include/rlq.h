@@ -217,6 +217,34 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
             int H, int I, const void *packed_gu, const void *packed_dn, int scale_dtype, float *h, int h_stride,
             void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---------------------------------------------------------------- native experts */
+
+/* The experts of one kind (gate_up or down) in the native format, one launch: replaces
+ * linear_q4n_moe (kernels/linear.metal:254-308; MoeLinearParams, kernels/params.h:28-31),
+ * which src/engine.mm:1019-1048 dispatches twice per MoE layer. The matrices sit in
+ * n_slots slots of Ne rows each (the stacked tensor, slot = expert, or an expert cache),
+ * packed together with rlq_pack_codes(w, K, n_slots*Ne, ...) or rlq_pack_native_blocked,
+ * with one fp32 scale per row s[n_slots*Ne]. For work item i < *n_items of
+ * items[max_items][4] = (e, r0, rows, 0) (rlq_moe_route writes them):
+ *   c[r0+j][n] = s[slot*Ne + n] * (a[src(r0+j)] . L(q[slot*Ne + n])^T),  slot = slots[e],
+ * for j < rows and n < Ne, with src(r) = tok[r] (a holds the T tokens: the gather of
+ * kernels/moe.metal:143-155 fused) or, tok == NULL, src(r) = r (a holds sorted rows, as
+ * act does). a fp16 [a_rows][a_stride], already multiplied by the matrix's column scale
+ * (the reference folds it upstream); c fp32 [.][c_stride]. book: RLQ_BOOK_INT15 or
+ * RLQ_BOOK_FP4 (the reference's W_T for experts; its expert kernel has no int16 half
+ * step, so RLQ_BOOK_INT16 is refused). A slot outside [0, n_slots) gives zero rows.
+ * K a multiple of 64 up to 24576, Ne a multiple of 16. */
+int rlq_moe_linear_native(const void *a, int a_stride, int a_rows, const int *tok, int K, int Ne, const void *packed,
+                          const float *s, const int *slots, int n_slots, int book, const int *items, const int *n_items,
+                          int max_items, float *c, int c_stride, void *stream);
+
+/* act[r][i] = half(silu(gu[r][i]) * gu[r][I + i] * cs[i]) for r < A, i < I: the SwiGLU of
+ * kernels/ops.metal:446-455 between the native gate_up and down products. cs is the down
+ * matrix's column scale (fp32 [I]; NULL means ones, as for affine matrices). gu fp32
+ * [A][gu_stride >= 2I]; act fp16 [A][act_stride]. */
+int rlq_moe_swiglu(const float *gu, int gu_stride, int A, int I, const float *cs, void *act, int act_stride,
+                   void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,19 +1,20 @@
 """Oracle for the mixture-of-experts part of the path: routing, gather, SwiGLU, combine.
 
 TEST INFRASTRUCTURE ONLY (see oracle/q4.py). Restated from kernels/moe.metal and
-kernels/ops.metal:446-455 of the reference; the grouped expert matmuls use the
-affine product of oracle/q4.py, which is what the BASELINE MoE config asks for
-(the reference's own MoE files are native q4n; the item/slot scheme is the same,
-kernels/linear.metal:254-308).
+kernels/ops.metal:446-455 of the reference. The grouped expert matmuls come in two
+forms: the affine product of oracle/q4.py, which is what the BASELINE MoE config asks
+for, and the native q4n product with the slot table of linear_q4n_moe
+(kernels/linear.metal:254-308; the reference's own MoE files are native).
 """
 
 from __future__ import annotations
 
 import numpy as np
 
-from .q4 import GROUP, linear_affine_f64, scale_to_f32
+from .q4 import GROUP, LEVELS, linear_affine_f64, linear_native_f64, scale_to_f32
 
-__all__ = ["moe_route", "moe_items", "silu", "swiglu_f16", "moe_layer_f64", "expert_rows"]
+__all__ = ["moe_route", "moe_items", "silu", "swiglu_f16", "moe_layer_f64", "expert_rows",
+           "moe_linear_native_f64", "moe_layer_native_f64"]
 
 
 def moe_route(logits, E: int, topk: int, norm_topk: bool = True):
@@ -114,4 +115,59 @@ def moe_layer_f64(x, logits, gu, dn, E: int, topk: int, I: int, H: int, norm_top
             a = swiglu_f16(g, I) if act_f16 else (silu(g[:, :I]) * g[:, I:])
             y = linear_affine_f64(np.asarray(a, np.float64), qd[rd], sd[rd], bd[rd], scale_dtype)
             h[t] += w[t * S + s] * y[0]
+    return h, sel, w
+
+
+# ------------------------------------------------------------------ native experts
+
+def moe_linear_native_f64(a, items, n_items: int, slots, codes, s_row, Ne: int, book: str, tok=None, n_rows=None):
+    """linear_q4n_moe (kernels/linear.metal:254-308) in float64: for work item i < n_items,
+    (e, r0, rows) = items[i], slot = slots[e],
+
+        C[r0+j][n] = s[slot*Ne + n] * (A[src(r0+j)] . L(q[slot*Ne + n])^T),  j < rows, n < Ne,
+
+    src(r) = tok[r] when tok is given (the gather of moe.metal:143-155, a holds the tokens),
+    else r. codes [n_slots*Ne][K] (0..15), s_row [n_slots*Ne]. Rows no item covers stay 0;
+    a slot outside [0, n_slots) gives zero rows. Returns C [n_rows][Ne] float64."""
+    a = np.asarray(a, dtype=np.float64)
+    codes = np.asarray(codes)
+    s_row = np.asarray(s_row, np.float64)
+    n_slots = codes.shape[0] // Ne
+    L = LEVELS[book].astype(np.float64)
+    if n_rows is None:
+        n_rows = int(max((int(it[1]) + int(it[2]) for it in np.asarray(items)[:n_items]), default=0))
+    C = np.zeros((n_rows, Ne), dtype=np.float64)
+    for e, r0, rows, _ in np.asarray(items)[:n_items]:
+        slot = int(slots[int(e)])
+        if not 0 <= slot < n_slots:
+            continue
+        W = L[codes[slot * Ne:(slot + 1) * Ne]]                     # [Ne][K]
+        src = [int(tok[r]) if tok is not None else r for r in range(int(r0), int(r0) + int(rows))]
+        C[int(r0):int(r0) + int(rows)] = (a[src] @ W.T) * s_row[slot * Ne:(slot + 1) * Ne][None, :]
+    return C
+
+
+def moe_layer_native_f64(x, logits, gu, dn, cs, slots, E: int, topk: int, I: int, H: int, book: str,
+                         norm_topk: bool = True, h0=None):
+    """The native MoE MLP of src/engine.mm:965-1059 (route, gather, linear_q4n_moe,
+    swiglu with the down matrix's column scale, linear_q4n_moe, combine), token by token
+    in float64 except the SwiGLU output, stored as half (ops.metal:454).
+
+    x: [T][H] fp16 (already times gate_up's column scale, as the reference folds it);
+    gu = (codes [n_slots*2I][H], s [n_slots*2I]): gate rows then up rows per slot;
+    dn = (codes [n_slots*H][I], s [n_slots*H]); cs [I] or None; slots [E+1].
+    Returns (h [T][H] float64, sel, w)."""
+    x = np.asarray(x)
+    T = x.shape[0]
+    S = topk + 1
+    sel, w = moe_route(logits, E, topk, norm_topk)
+    h = np.zeros((T, H), dtype=np.float64) if h0 is None else np.asarray(h0, np.float64).copy()
+    (qg, sg), (qd, sd) = gu, dn
+    for t in range(T):
+        for j in range(S):
+            slot = int(slots[int(sel[t * S + j])])
+            g = linear_native_f64(x[t:t + 1], qg[expert_rows(slot, 2 * I)], sg[expert_rows(slot, 2 * I)], book)
+            a = swiglu_f16(g, I, cs)
+            y = linear_native_f64(a, qd[expert_rows(slot, H)], sd[expert_rows(slot, H)], book)
+            h[t] += w[t * S + j] * y[0]
     return h, sel, w

@@ -892,6 +892,89 @@ static int route_gate_up_one_token(const MoeArgs &a, int sd, const float *logits
                        : launch_one_token_epl<16, 1>(epl, a, logits, E, topk, norm_topk, sel, w, tok, inv, items, n_items, st);
 }
 
+
+// ------------------------------------------------------------------ native experts
+
+// The experts of one kind in the native format, all in one launch (linear_q4n_moe,
+// kernels/linear.metal:254-308): grid (Ne / 16 tiles, max_items); item i < *n_items, for
+// expert e = items[i].x, reads slot = slots[e] (where the expert's matrix sits: the stacked
+// tensor, slot = expert, or an expert cache) and computes its 16-row tile blockIdx.x:
+//   c[r][n] = s[slot * Ne + n] * (a[src(r)] . L(q_slot[n])^T)   for the item's rows r
+// with src(r) = tok[r] (GATHER: the gather of moe.metal:143-155 fused, a holds the tokens)
+// or r (a holds sorted rows). Waves split K as in the affine expert kernel (expert_gpw)
+// and meet in LDS in wave order; no per-group scale, so each wave's products chain in
+// the MFMA (native_step) and the row scale is applied at the store, as the reference
+// applies it to its matmul result. A slot outside [0, n_slots) reads nothing and gives
+// zero rows.
+template <int GPW, int BOOK, bool GATHER>
+__global__ __launch_bounds__(1024) void moe_native_kernel(const _Float16 *a, int a_stride, int a_rows, const int *tok,
+                                                          int K, int Ne, const u32x4 *codes, const float *s,
+                                                          const int *slots, int n_slots, const int4 *items,
+                                                          const int *n_items_p, float *c, int c_stride) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int item = blockIdx.y;
+  // the list holds max_items entries (the grid's height), so the read is in bounds
+  const int4 it = items[item];
+  const int n_items = *n_items_p;
+  asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
+  if (item >= n_items) return;                  // uniform: the whole workgroup leaves
+  const int r0 = it.y, rows = it.z;
+  const int slot = __builtin_amdgcn_readfirstlane(slots[it.x]);
+  const int waves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, j4 = lane >> 4;
+  const int n = 16 * blockIdx.x + c16;
+  if (slot < 0 || slot >= n_slots) {            // uniform
+    if (wave == 0)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (4 * j4 + v < rows) c[(size_t)(r0 + 4 * j4 + v) * c_stride + n] = 0.0f;
+    return;
+  }
+  const int G = K / kGroup, G4 = quads_of(K);
+  const int wg0 = wave * GPW;
+  const int wn = max(0, min(G, wg0 + GPW) - wg0);
+  const WaveTile wt = wave_tile(codes, codes, slot * (Ne / 16) + (int)blockIdx.x, G4, wg0, GPW);
+  const bool live = c16 < rows;
+  int xrow = r0 + (live ? c16 : 0);
+  if constexpr (GATHER) xrow = min(max(tok[xrow], 0), a_rows - 1);
+  const uint32_t xrange = wn > 0 ? (uint32_t)((a_rows - 1) * a_stride + wn * kGroup) * 2u : 0u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a + (size_t)min(wg0, G) * kGroup, xrange);
+  f32x4 acc = tile_dot_rows<GPW, 0, BOOK>(wt, rx, (uint32_t)xrow * a_stride * 2u + 16u * j4, live, wn, lane);
+  acc = reduce_waves(acc, reinterpret_cast<f32x4 *>(lds), wave, waves, lane);
+  if (wave != 0) return;
+  const float sn = s[(size_t)slot * Ne + n];
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    if (4 * j4 + v < rows) c[(size_t)(r0 + 4 * j4 + v) * c_stride + n] = sn * acc[v];
+}
+
+// act[r][i] = half(silu(gu[r][i]) * gu[r][I + i] * cs[i]) (kernels/ops.metal:446-455); cs is
+// the down projection's column scale (ones for affine matrices: cs == nullptr).
+__global__ void moe_swiglu_kernel(const float *gu, int gu_stride, int A, int I, const float *cs, _Float16 *act,
+                                  int act_stride) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+  if (i >= I || r >= A) return;
+  const float *row = gu + (size_t)r * gu_stride;
+  const float v = silu(row[i]) * row[I + i];
+  act[(size_t)r * act_stride + i] = static_cast<_Float16>(cs ? v * cs[i] : v);
+}
+
+template <int GPW, int BOOK>
+static void launch_native_inst(dim3 grid, int threads, bool gather, hipStream_t st, const _Float16 *a, int a_stride,
+                               int a_rows, const int *tok, int K, int Ne, const u32x4 *codes, const float *s,
+                               const int *slots, int n_slots, const int4 *items, const int *n_items, float *c,
+                               int c_stride) {
+  const size_t lds = (size_t)(threads / 64 - 1) * 64 * 16;
+  if (gather)
+    moe_native_kernel<GPW, BOOK, true><<<grid, threads, lds, st>>>(a, a_stride, a_rows, tok, K, Ne, codes, s, slots,
+                                                                   n_slots, items, n_items, c, c_stride);
+  else
+    moe_native_kernel<GPW, BOOK, false><<<grid, threads, lds, st>>>(a, a_stride, a_rows, tok, K, Ne, codes, s, slots,
+                                                                    n_slots, items, n_items, c, c_stride);
+}
+
 }  // namespace rlq
 
 using namespace rlq;
@@ -1068,6 +1151,65 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
   }
   if (int rc = rlq_moe_down(act, I, T, H, I, E, topk, packed_dn, scale_dtype, items, n_items, y, H, stream)) return rc;
   return rlq_moe_combine(y, H, inv, w, T, topk, H, h, h_stride, stream);
+}
+
+
+int rlq_moe_linear_native(const void *a, int a_stride, int a_rows, const int *tok, int K, int Ne, const void *packed,
+                          const float *s, const int *slots, int n_slots, int book, const int *items, const int *n_items,
+                          int max_items, float *c, int c_stride, void *stream) {
+  using namespace rlq;
+  RLQ_REQUIRE(a && packed && s && slots && items && n_items && c, "rlq_moe_linear_native: null pointer argument");
+  RLQ_REQUIRE(book == RLQ_BOOK_INT15 || book == RLQ_BOOK_FP4,
+              "rlq_moe_linear_native: book %d (int15 or fp4; the reference's expert kernel has no int16 half step)",
+              book);
+  RLQ_REQUIRE(K >= kGroup && K % kGroup == 0 && K <= 16 * 24 * kGroup,
+              "rlq_moe_linear_native: K=%d must be a multiple of 64 and <= %d", K, 16 * 24 * kGroup);
+  RLQ_REQUIRE(Ne >= 16 && Ne % 16 == 0, "rlq_moe_linear_native: Ne=%d must be a multiple of 16", Ne);
+  RLQ_REQUIRE(n_slots >= 1 && (long long)n_slots * Ne <= (1LL << 30), "rlq_moe_linear_native: %d slots of %d rows",
+              n_slots, Ne);
+  RLQ_REQUIRE(a_rows >= 1 && a_stride >= K && a_stride % 8 == 0 && aligned(a, 16) && aligned(packed, 16),
+              "rlq_moe_linear_native: a must be 16-byte aligned rows of >= K halves (a_rows=%d a_stride=%d)", a_rows,
+              a_stride);
+  RLQ_REQUIRE((long long)a_rows * a_stride * 2 < (1LL << 31), "rlq_moe_linear_native: a is too large");
+  RLQ_REQUIRE(c_stride >= Ne && max_items >= 0, "rlq_moe_linear_native: c_stride=%d < Ne=%d or max_items=%d",
+              c_stride, Ne, max_items);
+  RLQ_REQUIRE(aligned(items, 16), "rlq_moe_linear_native: items must be 16-byte aligned");
+  if (max_items == 0) return 0;
+  const dim3 grid(Ne / 16, max_items);
+  const int gpw = expert_gpw(K), threads = 64 * expert_waves(K);
+  auto st = static_cast<hipStream_t>(stream);
+  auto ah = static_cast<const _Float16 *>(a);
+  auto codes = static_cast<const u32x4 *>(packed);
+  auto it = reinterpret_cast<const int4 *>(items);
+  const bool gather = tok != nullptr;
+#define RLQ_NATIVE(G, B) \
+  launch_native_inst<G, B>(grid, threads, gather, st, ah, a_stride, a_rows, tok, K, Ne, codes, s, slots, n_slots, it, \
+                           n_items, c, c_stride)
+  if (book == RLQ_BOOK_INT15) {
+    if (gpw == 8) RLQ_NATIVE(8, kInt15);
+    else if (gpw == 16) RLQ_NATIVE(16, kInt15);
+    else RLQ_NATIVE(24, kInt15);
+  } else {
+    if (gpw == 8) RLQ_NATIVE(8, kFp4);
+    else if (gpw == 16) RLQ_NATIVE(16, kFp4);
+    else RLQ_NATIVE(24, kFp4);
+  }
+#undef RLQ_NATIVE
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+int rlq_moe_swiglu(const float *gu, int gu_stride, int A, int I, const float *cs, void *act, int act_stride,
+                   void *stream) {
+  using namespace rlq;
+  RLQ_REQUIRE(gu && act, "rlq_moe_swiglu: null pointer argument");
+  RLQ_REQUIRE(A >= 0 && I >= 1 && gu_stride >= 2 * I && act_stride >= I,
+              "rlq_moe_swiglu: A=%d I=%d gu_stride=%d act_stride=%d", A, I, gu_stride, act_stride);
+  if (A == 0) return 0;
+  moe_swiglu_kernel<<<dim3((I + 255) / 256, A), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      gu, gu_stride, A, I, cs, static_cast<_Float16 *>(act), act_stride);
+  RLQ_HIP(hipGetLastError());
+  return 0;
 }
 
 }  // extern "C"

@@ -377,3 +377,75 @@ def moe(x: torch.Tensor, logits: torch.Tensor, mw: MoeWeights, topk: int, h: tor
              mw.H, mw.I, _ptr(mw.gate_up.packed), _ptr(mw.down.packed), mw.gate_up.code, _ptr(h), h.stride(0), _ptr(ws),
              ws.numel(), _stream(stream))
     return h
+
+
+# ------------------------------------------------------------------ native experts
+
+@dataclass
+class MoeNativeStack:
+    """One kind of expert matrices (gate_up or down) in the native format: n_slots slots of
+    Ne rows each (the stacked tensor, slot = expert, or an expert cache), codes in the tile
+    layout and one fp32 scale per row (kernels/linear.metal:254-308)."""
+    packed: torch.Tensor     # uint8, rlq_packed_codes_bytes(K, n_slots * Ne)
+    s_row: torch.Tensor      # float32 [n_slots * Ne]
+    K: int
+    Ne: int
+    n_slots: int
+    book: str
+
+    @property
+    def code(self) -> int:
+        return BOOKS[self.book]
+
+
+def pack_moe_native(w: torch.Tensor, s_row: torch.Tensor, Ne: int, book: str, stream=None) -> MoeNativeStack:
+    """Row-major codes of the stacked tensor (32-bit words [n_slots*Ne][K/8]) -> MoeNativeStack."""
+    nw = pack_native(w, s_row, book, stream=stream)
+    if nw.N % Ne:
+        raise ValueError(f"{nw.N} rows is not a whole number of {Ne}-row slots")
+    return MoeNativeStack(nw.packed, nw.s_row, nw.K, Ne, nw.N // Ne, book)
+
+
+def moe_linear_native(a: torch.Tensor, st: MoeNativeStack, slots: torch.Tensor, r: MoeRouting, gather: bool,
+                      out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """c fp32 [T*S][Ne]: each sorted row times its expert's slot (rlq_moe_linear_native);
+    gather: a holds the T tokens and row r reads token tok[r], else a holds sorted rows."""
+    if a.dtype != torch.float16 or a.dim() != 2 or a.stride(1) != 1 or a.shape[1] < st.K:
+        raise ValueError("a must be a row-major float16 matrix of >= K columns")
+    if slots.dtype != torch.int32 or not slots.is_contiguous():
+        raise ValueError("slots must be a contiguous int32 vector [E+1]")
+    A = r.T * (r.topk + 1)
+    if out is None:
+        out = torch.empty((A, st.Ne), dtype=torch.float32, device=a.device)
+    lib.call("rlq_moe_linear_native", _ptr(a), a.stride(0), a.shape[0], _ptr(r.tok) if gather else 0, st.K, st.Ne,
+             _ptr(st.packed), _ptr(st.s_row), _ptr(slots), st.n_slots, st.code, _ptr(r.items), _ptr(r.n_items),
+             r.items.shape[0], _ptr(out), out.stride(0), _stream(stream))
+    return out
+
+
+def moe_swiglu(gu: torch.Tensor, I: int, cs: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """act fp16 [A][I] = half(silu(g) * u * cs) (rlq_moe_swiglu)."""
+    if gu.dtype != torch.float32 or gu.dim() != 2 or gu.stride(1) != 1:
+        raise ValueError("gu must be a row-major float32 matrix")
+    if cs is not None and (cs.dtype != torch.float32 or not cs.is_contiguous() or cs.numel() < I):
+        raise ValueError("cs must be a contiguous float32 vector of >= I column scales")
+    act = torch.empty((gu.shape[0], I), dtype=torch.float16, device=gu.device)
+    lib.call("rlq_moe_swiglu", _ptr(gu), gu.stride(0), gu.shape[0], I, _ptr(cs) if cs is not None else 0, _ptr(act),
+             act.stride(0), _stream(stream))
+    return act
+
+
+def moe_native(x: torch.Tensor, logits: torch.Tensor, gu: MoeNativeStack, dn: MoeNativeStack, slots: torch.Tensor,
+               topk: int, h: torch.Tensor, cs: torch.Tensor | None = None, norm_topk: bool = True,
+               stream=None) -> torch.Tensor:
+    """The native MoE MLP in the reference's order (src/engine.mm:965-1059): route, gate_up
+    product with the gather fused, SwiGLU with the down matrix's column scale cs, down
+    product, combine into h. x is already times gate_up's column scale."""
+    E = slots.numel() - 1
+    if gu.Ne % 2 or dn.K != gu.Ne // 2 or dn.Ne != gu.K:
+        raise ValueError("gate_up [2I][H] and down [H][I] stacks do not match")
+    r = moe_route(logits, E, topk, norm_topk, stream=stream)
+    g = moe_linear_native(x, gu, slots, r, True, stream=stream)
+    act = moe_swiglu(g, gu.Ne // 2, cs, stream=stream)
+    y = moe_linear_native(act, dn, slots, r, False, stream=stream)
+    return moe_combine(y, r, h, stream=stream)

@@ -86,3 +86,70 @@ def test_moe_layer_linearity_in_h0_and_weights():
         a = (g[:I] / (1 + np.exp(-g[:I])) * g[I:]).astype(np.float16).astype(np.float64)
         acc += w[t * S + s] * (a @ Wde.T)
     np.testing.assert_allclose(h[t], acc, rtol=1e-9, atol=1e-12)
+
+
+def _native_stack(rng, n_slots, Ne, K):
+    codes = rng.integers(0, 16, size=(n_slots * Ne, K), dtype=np.uint8)
+    s_row = rng.uniform(0.01, 0.03, size=n_slots * Ne).astype(np.float32)
+    return codes, s_row
+
+
+def test_native_expert_product_follows_the_slot_table():
+    """Moving the experts to other slots and the table with them leaves every product
+    unchanged (a kernel that indexed by expert instead of slot would not); with the
+    identity table an item's rows are the plain native product of its expert's rows."""
+    rng = np.random.default_rng(3)
+    E, Ne, K, T, topk = 6, 32, 128, 5, 2
+    codes, s_row = _native_stack(rng, E + 1, Ne, K)
+    x = rng.standard_normal((T, K)).astype(np.float16)
+    sel, _ = O.moe_route(rng.standard_normal((T, E + 1)).astype(np.float32), E, topk)
+    _, off, items = O.moe_items(sel, E, 16)
+    S = topk + 1
+    # the sorted rows' tokens: rows of an expert in token order
+    tok = np.zeros(T * S, dtype=np.int64)
+    for e in range(E + 1):
+        tok[off[e]:off[e + 1]] = np.flatnonzero(sel == e) // S
+    ident = np.arange(E + 1)
+    C = O.moe_linear_native_f64(x, items, len(items), ident, codes, s_row, Ne, "int15", tok=tok, n_rows=T * S)
+    for e, r0, rows, _ in items:
+        ref = O.linear_native_f64(x[tok[r0:r0 + rows]], codes[e * Ne:(e + 1) * Ne], s_row[e * Ne:(e + 1) * Ne], "int15")
+        np.testing.assert_allclose(C[r0:r0 + rows], ref, rtol=1e-12, atol=1e-12)
+    perm = rng.permutation(E + 3)[:E + 1]          # slots in a larger cache, some left empty
+    codes2 = np.zeros(((E + 3) * Ne, K), dtype=np.uint8)
+    s2 = np.zeros((E + 3) * Ne, dtype=np.float32)
+    for e in range(E + 1):
+        codes2[perm[e] * Ne:(perm[e] + 1) * Ne] = codes[e * Ne:(e + 1) * Ne]
+        s2[perm[e] * Ne:(perm[e] + 1) * Ne] = s_row[e * Ne:(e + 1) * Ne]
+    C2 = O.moe_linear_native_f64(x, items, len(items), perm, codes2, s2, Ne, "int15", tok=tok, n_rows=T * S)
+    np.testing.assert_array_equal(C2, C)
+
+
+def test_native_layer_token_loop_equals_sorted_pipeline():
+    """The token-by-token native layer equals the reference's sorted pipeline (route,
+    items, gathered gate_up product, SwiGLU with the column scale, down product over
+    sorted rows, combine in slot order), both in float64 with act stored as half."""
+    rng = np.random.default_rng(4)
+    E, H, I, T, topk = 5, 64, 64, 7, 2
+    S = topk + 1
+    gq, gs = _native_stack(rng, E + 1, 2 * I, H)
+    dq, ds = _native_stack(rng, E + 1, H, I)
+    cs = rng.uniform(0.5, 1.5, size=I).astype(np.float32)
+    slots = np.arange(E + 1)[::-1].copy()          # expert e stored in slot E - e
+    x = (rng.standard_normal((T, H)) * 0.5).astype(np.float16)
+    logits = rng.standard_normal((T, E + 1)).astype(np.float32)
+    h, sel, w = O.moe_layer_native_f64(x, logits, (gq, gs), (dq, ds), cs, slots, E, topk, I, H, "fp4")
+    _, off, items = O.moe_items(sel, E, 16)
+    tok = np.zeros(T * S, dtype=np.int64)
+    inv = np.zeros(T * S, dtype=np.int64)
+    for e in range(E + 1):
+        a_e = np.flatnonzero(sel == e)
+        tok[off[e]:off[e + 1]] = a_e // S
+        inv[a_e] = np.arange(off[e], off[e + 1])
+    gu = O.moe_linear_native_f64(x, items, len(items), slots, gq, gs, 2 * I, "fp4", tok=tok, n_rows=T * S)
+    act = O.swiglu_f16(gu, I, cs)
+    y = O.moe_linear_native_f64(act, items, len(items), slots, dq, ds, H, "fp4", n_rows=T * S)
+    h2 = np.zeros((T, H))
+    for t in range(T):
+        for j in range(S):
+            h2[t] += w[t * S + j] * y[inv[t * S + j]]
+    np.testing.assert_allclose(h2, h, rtol=1e-9, atol=1e-12)

@@ -210,6 +210,61 @@ def bench_moe(device, steps, warmup):
         del sg
     del mws
     torch.cuda.empty_cache()
+    out.update(bench_moe_native(device, steps, warmup))
+    return out
+
+
+NATIVE_EXPERT_BYTES = 1585152   # int15 codes + fp32 row scales of one expert's gate_up [1024][2048] and down [2048][512]
+
+
+def bench_moe_native(device, steps, warmup):
+    """The same MoE layer in the reference's own expert format (kernels/linear.metal:254-308):
+    native int15 codes with an fp32 scale per row, slot = expert, the down matrix's column
+    scale applied in the SwiGLU. One step = route, gate_up product (gather fused), SwiGLU,
+    down product, combine. Bytes: distinct_experts * 1,585,152 + A*(2H + 2*2I*4 + 2*I*2 +
+    2*H*4) (x rows read; gate_up, act and y each written and read once)."""
+    import torch
+
+    from raceline_amd import ops, synth
+    from raceline_amd.configs import MOE
+
+    E, H, I, topk = MOE["E"], MOE["H"], MOE["I"], MOE["topk"]
+    per_copy = (E + 1) * NATIVE_EXPERT_BYTES
+    copies = max(2, -(-CACHE_DEFEAT_BYTES // per_copy))
+    log(f"[bench] building {copies} copies of the native MoE experts ({per_copy / 1e6:.1f} MB each)")
+    stacks = []
+    for c in range(copies):
+        g = torch.Generator(device=device)
+        g.manual_seed(700 + c)
+        lo, hi = -(1 << 31), (1 << 31) - 1
+        gw = torch.randint(lo, hi, ((E + 1) * 2 * I, H // 8), generator=g, device=device, dtype=torch.int32)
+        dw = torch.randint(lo, hi, ((E + 1) * H, I // 8), generator=g, device=device, dtype=torch.int32)
+        gs = torch.rand((E + 1) * 2 * I, generator=g, device=device) * 0.004 + 0.001
+        ds = torch.rand((E + 1) * H, generator=g, device=device) * 0.004 + 0.001
+        stacks.append((ops.pack_moe_native(gw, gs, 2 * I, "int15"), ops.pack_moe_native(dw, ds, H, "int15")))
+        del gw, dw
+    slots = torch.arange(E + 1, dtype=torch.int32, device=device)
+    g = torch.Generator(device=device)
+    g.manual_seed(800)
+    cs = torch.rand(I, generator=g, device=device) + 0.5
+    out = {}
+    for T in MOE["tokens"]:
+        x = synth.random_activations(T, H, 600 + T, device)
+        g.manual_seed(601 + T)
+        logits = torch.randn((T, E + 1), generator=g, device=device, dtype=torch.float32)
+        h = torch.zeros((T, H), dtype=torch.float32, device=device)
+        fns = [(lambda gu=gu, dn=dn: ops.moe_native(x, logits, gu, dn, slots, topk, h, cs=cs)) for gu, dn in stacks]
+        sg = StepGraphs(fns)
+        t = time_steps(sg, steps, warmup)
+        distinct = int(torch.unique(ops.moe_route(logits, E, topk).sel).numel())
+        A = T * (topk + 1)
+        nbytes = distinct * NATIVE_EXPERT_BYTES + A * (2 * H + 2 * 2 * I * 4 + 2 * I * 2 + 2 * H * 4)
+        out[f"moe_native_t{T}"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
+                                   "distinct_experts": distinct, "algorithmic_bytes": nbytes, "book": "int15"}
+        log(f"[bench] native MoE T={T}: {t * 1e6:.1f} us/step, {nbytes / t / 1e9:.0f} GB/s ({distinct} experts)")
+        del sg
+    del stacks
+    torch.cuda.empty_cache()
     return out
 
 

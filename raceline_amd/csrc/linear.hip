@@ -524,6 +524,7 @@ static int pack_mlx(const char *who, const uint32_t *w, const void *s, const voi
   RLQ_REQUIRE(aligned(w, 4) && aligned(packed, 16), "%s: misaligned w or packed", who);
   RLQ_REQUIRE(aligned(s, 2) && aligned(b, 2), "%s: misaligned scales or biases", who);
   const size_t pieces = (size_t)tiles_of(N) * 2 * quads_of(K) * 64;
+  RLQ_REQUIRE(pieces < (1ull << 31), "%s: K=%d N=%d is too large to pack in one launch", who, K, N);
   auto codes = static_cast<u32x4 *>(packed);
   auto sb = reinterpret_cast<u32x4 *>(static_cast<char *>(packed) + packed_code_bytes(K, N));
   pack_mlx_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
@@ -568,11 +569,13 @@ size_t rlq_packed_codes_bytes(int K, int N) {
 }
 
 int rlq_pack_codes(const uint32_t *w, int K, int N, void *packed, void *stream) {
+  // N is not limited to what one linear call takes: an expert stack (rlq_moe_linear_native)
+  // can hold more rows than that
   RLQ_REQUIRE(N >= 1 && K >= kGroup && K % kGroup == 0, "rlq_pack_codes: bad sizes K=%d N=%d", K, N);
-  RLQ_REQUIRE(N <= 16 * kMaxTiles, "rlq_pack_codes: N=%d exceeds the supported %d", N, 16 * kMaxTiles);
   RLQ_REQUIRE(w && packed, "rlq_pack_codes: null pointer argument");
   RLQ_REQUIRE(aligned(w, 4) && aligned(packed, 16), "rlq_pack_codes: misaligned w or packed");
   const size_t pieces = (size_t)tiles_of(N) * 2 * quads_of(K) * 64;
+  RLQ_REQUIRE(pieces < (1ull << 31), "rlq_pack_codes: K=%d N=%d is too large to pack in one launch", K, N);
   pack_mlx_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
       w, nullptr, nullptr, K, N, 0, static_cast<u32x4 *>(packed), nullptr);
   RLQ_HIP(hipGetLastError());

@@ -220,9 +220,9 @@ NATIVE_EXPERT_BYTES = 1585152   # int15 codes + fp32 row scales of one expert's 
 def bench_moe_native(device, steps, warmup):
     """The same MoE layer in the reference's own expert format (kernels/linear.metal:254-308):
     native int15 codes with an fp32 scale per row, slot = expert, the down matrix's column
-    scale applied in the SwiGLU. One step = route, gate_up product (gather fused), SwiGLU,
-    down product, combine. Bytes: distinct_experts * 1,585,152 + A*(2H + 2*2I*4 + 2*I*2 +
-    2*H*4) (x rows read; gate_up, act and y each written and read once)."""
+    scale applied in the SwiGLU. One step = route, gate_up product with the gather and the
+    SwiGLU fused, down product, combine. Bytes: distinct_experts * 1,585,152 +
+    A*(2H + 2*I*2 + 2*H*4) (x rows read; act and y each written and read once)."""
     import torch
 
     from raceline_amd import ops, synth
@@ -258,7 +258,7 @@ def bench_moe_native(device, steps, warmup):
         t = time_steps(sg, steps, warmup)
         distinct = int(torch.unique(ops.moe_route(logits, E, topk).sel).numel())
         A = T * (topk + 1)
-        nbytes = distinct * NATIVE_EXPERT_BYTES + A * (2 * H + 2 * 2 * I * 4 + 2 * I * 2 + 2 * H * 4)
+        nbytes = distinct * NATIVE_EXPERT_BYTES + A * (2 * H + 2 * I * 2 + 2 * H * 4)
         out[f"moe_native_t{T}"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
                                    "distinct_experts": distinct, "algorithmic_bytes": nbytes, "book": "int15"}
         log(f"[bench] native MoE T={T}: {t * 1e6:.1f} us/step, {nbytes / t / 1e9:.0f} GB/s ({distinct} experts)")

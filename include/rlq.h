@@ -238,6 +238,17 @@ int rlq_moe_linear_native(const void *a, int a_stride, int a_rows, const int *to
                           const float *s, const int *slots, int n_slots, int book, const int *items, const int *n_items,
                           int max_items, float *c, int c_stride, void *stream);
 
+/* The native gate/up product with the SwiGLU folded in: for the items as above and the
+ * stacked gate_up tensor of n_slots slots of 2I rows (gate rows [0, I), up rows [I, 2I)),
+ *   act[r][i] = half(silu(g) * u * cs[i]),  g = gu-product row i, u = row I + i,
+ * the same bits as rlq_moe_linear_native (tok given) followed by rlq_moe_swiglu, in one
+ * launch and without the fp32 gate/up rows. x fp16 [T][x_stride] (the tokens, read
+ * through tok); act fp16 [T*S][act_stride]; cs as for rlq_moe_swiglu. I a multiple of 16. */
+int rlq_moe_gate_up_native(const void *x, int x_stride, int T, const int *tok, int H, int I, const void *packed_gu,
+                           const float *s_gu, const int *slots, int n_slots, int book, const int *items,
+                           const int *n_items, int max_items, const float *cs, void *act, int act_stride,
+                           void *stream);
+
 /* act[r][i] = half(silu(gu[r][i]) * gu[r][I + i] * cs[i]) for r < A, i < I: the SwiGLU of
  * kernels/ops.metal:446-455 between the native gate_up and down products. cs is the down
  * matrix's column scale (fp32 [I]; NULL means ones, as for affine matrices). gu fp32

@@ -975,6 +975,91 @@ static void launch_native_inst(dim3 grid, int threads, bool gather, hipStream_t 
                                                                     n_slots, items, n_items, c, c_stride);
 }
 
+
+// The native gate/up product with the SwiGLU in its epilogue: workgroup (i, item) takes
+// the gate tile i and the up tile i + I/16 of the item's expert slot (the reference's
+// gate rows [0, I) then up rows [I, 2I) of each expert), reads each activation operand
+// once for both (tile_dot_rows2: each tile's sums are tile_dot_rows's) and writes
+//   act[r][n] = half(silu(sg[n] * g) * (su[n] * u) * cs[n])
+// with the products and the order of moe_native_kernel followed by moe_swiglu_kernel, so
+// the bits are the two launches' without the fp32 gate/up rows in between. The gather is
+// fused (rows are read through tok).
+template <int GPW, int BOOK>
+__global__ __launch_bounds__(1024) void moe_native_gate_up_kernel(const _Float16 *x, int x_stride, int T,
+                                                                  const int *tok, int H, int I, const u32x4 *codes,
+                                                                  const float *s, const int *slots, int n_slots,
+                                                                  const int4 *items, const int *n_items_p,
+                                                                  const float *cs, _Float16 *act, int act_stride) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int item = blockIdx.y;
+  const int4 it = items[item];
+  const int n_items = *n_items_p;
+  asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
+  if (item >= n_items) return;                  // uniform: the whole workgroup leaves
+  const int r0 = it.y, rows = it.z;
+  const int slot = __builtin_amdgcn_readfirstlane(slots[it.x]);
+  const int waves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, j4 = lane >> 4;
+  const int n = 16 * blockIdx.x + c16;          // feature of the gate and up halves
+  if (slot < 0 || slot >= n_slots) {            // uniform: zero rows, as the two launches give
+    if (wave == 0)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (4 * j4 + v < rows) {
+          const float z = silu(0.0f) * 0.0f;
+          act[(size_t)(r0 + 4 * j4 + v) * act_stride + n] = static_cast<_Float16>(cs ? z * cs[n] : z);
+        }
+    return;
+  }
+  const int G = H / kGroup, G4 = quads_of(H);
+  const int wg0 = wave * GPW;
+  const int wn = max(0, min(G, wg0 + GPW) - wg0);
+  const int tg = slot * (2 * I / 16) + (int)blockIdx.x;
+  const WaveTile wgt = wave_tile(codes, codes, tg, G4, wg0, GPW);
+  const WaveTile wut = wave_tile(codes, codes, tg + I / 16, G4, wg0, GPW);
+  const bool live = c16 < rows;
+  const int xrow = min(max(tok[r0 + (live ? c16 : 0)], 0), T - 1);
+  const uint32_t xrange = wn > 0 ? (uint32_t)((T - 1) * x_stride + wn * kGroup) * 2u : 0u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)min(wg0, G) * kGroup, xrange);
+  f32x4 ag, au;
+  tile_dot_rows2<GPW, 0, BOOK>(wgt, wut, rx, (uint32_t)xrow * x_stride * 2u + 16u * j4, live, wn, lane, ag, au);
+  f32x4 *red = reinterpret_cast<f32x4 *>(lds);  // [2][waves-1][64]
+  if (wave > 0) {
+    red[(wave - 1) * 64 + lane] = ag;
+    red[(waves - 1 + wave - 1) * 64 + lane] = au;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w = 1; w < waves; ++w) {
+    const f32x4 og = red[(w - 1) * 64 + lane], ou = red[(waves - 1 + w - 1) * 64 + lane];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      ag[v] += og[v];
+      au[v] += ou[v];
+    }
+  }
+  const size_t srow = (size_t)slot * 2 * I + n;
+  const float sg = s[srow], su = s[srow + I];
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    if (4 * j4 + v < rows) {
+      const float z = silu(sg * ag[v]) * (su * au[v]);
+      act[(size_t)(r0 + 4 * j4 + v) * act_stride + n] = static_cast<_Float16>(cs ? z * cs[n] : z);
+    }
+}
+
+template <int GPW, int BOOK>
+static void launch_native_gate_up_inst(dim3 grid, int threads, hipStream_t st, const _Float16 *x, int x_stride, int T,
+                                       const int *tok, int H, int I, const u32x4 *codes, const float *s,
+                                       const int *slots, int n_slots, const int4 *items, const int *n_items,
+                                       const float *cs, _Float16 *act, int act_stride) {
+  const size_t lds = (size_t)2 * (threads / 64 - 1) * 64 * 16;
+  moe_native_gate_up_kernel<GPW, BOOK><<<grid, threads, lds, st>>>(x, x_stride, T, tok, H, I, codes, s, slots, n_slots,
+                                                                   items, n_items, cs, act, act_stride);
+}
+
 }  // namespace rlq
 
 using namespace rlq;
@@ -1208,6 +1293,51 @@ int rlq_moe_swiglu(const float *gu, int gu_stride, int A, int I, const float *cs
   if (A == 0) return 0;
   moe_swiglu_kernel<<<dim3((I + 255) / 256, A), 256, 0, static_cast<hipStream_t>(stream)>>>(
       gu, gu_stride, A, I, cs, static_cast<_Float16 *>(act), act_stride);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+
+int rlq_moe_gate_up_native(const void *x, int x_stride, int T, const int *tok, int H, int I, const void *packed_gu,
+                           const float *s_gu, const int *slots, int n_slots, int book, const int *items,
+                           const int *n_items, int max_items, const float *cs, void *act, int act_stride,
+                           void *stream) {
+  using namespace rlq;
+  RLQ_REQUIRE(x && tok && packed_gu && s_gu && slots && items && n_items && act,
+              "rlq_moe_gate_up_native: null pointer argument");
+  RLQ_REQUIRE(book == RLQ_BOOK_INT15 || book == RLQ_BOOK_FP4,
+              "rlq_moe_gate_up_native: book %d (int15 or fp4; the reference's expert kernel has no int16 half step)",
+              book);
+  RLQ_REQUIRE(H >= kGroup && H % kGroup == 0 && H <= 16 * 24 * kGroup,
+              "rlq_moe_gate_up_native: H=%d must be a multiple of 64 and <= %d", H, 16 * 24 * kGroup);
+  RLQ_REQUIRE(I >= 16 && I % 16 == 0 && act_stride >= I, "rlq_moe_gate_up_native: I=%d (a multiple of 16), act_stride=%d",
+              I, act_stride);
+  RLQ_REQUIRE(n_slots >= 1 && (long long)n_slots * 2 * I <= (1LL << 30), "rlq_moe_gate_up_native: %d slots", n_slots);
+  RLQ_REQUIRE(T >= 1 && x_stride >= H && x_stride % 8 == 0 && aligned(x, 16) && aligned(packed_gu, 16) &&
+                  aligned(items, 16),
+              "rlq_moe_gate_up_native: x must be 16-byte aligned rows of >= H halves (T=%d x_stride=%d)", T, x_stride);
+  RLQ_REQUIRE((long long)T * x_stride * 2 < (1LL << 31) && max_items >= 0, "rlq_moe_gate_up_native: x is too large");
+  if (max_items == 0) return 0;
+  const dim3 grid(I / 16, max_items);
+  const int gpw = expert_gpw(H), threads = 64 * expert_waves(H);
+  auto st = static_cast<hipStream_t>(stream);
+  auto xh = static_cast<const _Float16 *>(x);
+  auto codes = static_cast<const u32x4 *>(packed_gu);
+  auto it = reinterpret_cast<const int4 *>(items);
+  auto ah = static_cast<_Float16 *>(act);
+#define RLQ_NATIVE_GU(G, B) \
+  launch_native_gate_up_inst<G, B>(grid, threads, st, xh, x_stride, T, tok, H, I, codes, s_gu, slots, n_slots, it, \
+                                   n_items, cs, ah, act_stride)
+  if (book == RLQ_BOOK_INT15) {
+    if (gpw == 8) RLQ_NATIVE_GU(8, kInt15);
+    else if (gpw == 16) RLQ_NATIVE_GU(16, kInt15);
+    else RLQ_NATIVE_GU(24, kInt15);
+  } else {
+    if (gpw == 8) RLQ_NATIVE_GU(8, kFp4);
+    else if (gpw == 16) RLQ_NATIVE_GU(16, kFp4);
+    else RLQ_NATIVE_GU(24, kFp4);
+  }
+#undef RLQ_NATIVE_GU
   RLQ_HIP(hipGetLastError());
   return 0;
 }

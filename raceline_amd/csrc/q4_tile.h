@@ -246,6 +246,65 @@ __device__ __forceinline__ f32x4 tile_dot_rows(const WaveTile &w, __amdgpu_buffe
   return acc;
 }
 
+// tile_dot_rows for two tiles at once (the same groups of two weight tiles, w0 and w1, one
+// activation stream): every activation operand is loaded once and multiplied into both
+// tiles, and the activation-only terms (affine group sums, kInt16 activation sums) are
+// formed once. Each tile's products and sums are the ones tile_dot_rows forms, in the
+// same order, so acc0 and acc1 hold its bits.
+template <int GPW, int SD, int BOOK = kAffine>
+__device__ __forceinline__ void tile_dot_rows2(const WaveTile &w0, const WaveTile &w1, __amdgpu_buffer_rsrc_t rx,
+                                               uint32_t xoff, bool live, int wn, int lane, f32x4 &acc0, f32x4 &acc1) {
+  u32x4 wq0[GPW / 2], sq0[GPW / 4], wq1[GPW / 2], sq1[GPW / 4];
+  auto ldx = [&](int jg, int s) -> u32x4 {
+    const bool ok = live && jg < wn;
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rx, ok ? xoff + (uint32_t)(jg * kGroup + 32 * s) * 2u : kFarOffset, 0, 0));
+  };
+  u32x4 ax[3][2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) ax[d][s] = ldx(d, s);
+  issue_tile_loads<GPW, BOOK>(w0, lane, wq0, sq0);
+  issue_tile_loads<GPW, BOOK>(w1, lane, wq1, sq1);
+  __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before the first multiply
+  const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
+  f32x4 asum = {};
+  acc0 = f32x4{};
+  acc1 = f32x4{};
+#pragma unroll
+  for (int jg = 0; jg < GPW; ++jg) {
+    if (jg + 2 < GPW) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) ax[(jg + 2) % 3][s] = ldx(jg + 2, s);
+    }
+    const half8 af[2] = {__builtin_bit_cast(half8, prep_act<BOOK>(ax[jg % 3][0])),
+                         __builtin_bit_cast(half8, prep_act<BOOK>(ax[jg % 3][1]))};
+    if constexpr (BOOK == kAffine) {
+      const f32x4 gsv = group_sums(af);
+      group_step_gs<GPW, SD, 4>(acc0, af, gsv, wq0, sq0, jg);
+      group_step_gs<GPW, SD, 4>(acc1, af, gsv, wq1, sq1, jg);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq0[jg >> 1][2 * (jg & 1) + s]),
+                                                      acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq1[jg >> 1][2 * (jg & 1) + s]),
+                                                      acc1, 0, 0, 0);
+        if constexpr (BOOK == kInt16) asum = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, asum, 0, 0, 0);
+      }
+    }
+    asm volatile("" : "+v"(acc0), "+v"(acc1));   // each group's epilogue stays with its group
+  }
+  if constexpr (BOOK == kInt16) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      acc0[v] = __builtin_fmaf(0.5f, asum[v], acc0[v]);
+      acc1[v] = __builtin_fmaf(0.5f, asum[v], acc1[v]);
+    }
+  }
+}
+
 // LDS bytes of one staged activation row of an 8-group wave range: its 64 chunks of 16
 // bytes, chunk c of row r at position c ^ (r & 15), so the 16 rows a wave reads at once
 // (the same chunk of each) fall in different banks without padding.

@@ -435,17 +435,36 @@ def moe_swiglu(gu: torch.Tensor, I: int, cs: torch.Tensor | None = None, stream=
     return act
 
 
+def moe_gate_up_native(x: torch.Tensor, gu: MoeNativeStack, slots: torch.Tensor, r: MoeRouting,
+                       cs: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """act fp16 [T*S][I]: the gathered gate/up product and the SwiGLU in one launch
+    (rlq_moe_gate_up_native; the bits of moe_linear_native + moe_swiglu)."""
+    if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < gu.K:
+        raise ValueError("x must be a row-major float16 [T][>= H] matrix")
+    if cs is not None and (cs.dtype != torch.float32 or not cs.is_contiguous() or cs.numel() < gu.Ne // 2):
+        raise ValueError("cs must be a contiguous float32 vector of >= I column scales")
+    I = gu.Ne // 2
+    act = torch.empty((r.T * (r.topk + 1), I), dtype=torch.float16, device=x.device)
+    lib.call("rlq_moe_gate_up_native", _ptr(x), x.stride(0), x.shape[0], _ptr(r.tok), gu.K, I, _ptr(gu.packed),
+             _ptr(gu.s_row), _ptr(slots), gu.n_slots, gu.code, _ptr(r.items), _ptr(r.n_items), r.items.shape[0],
+             _ptr(cs) if cs is not None else 0, _ptr(act), act.stride(0), _stream(stream))
+    return act
+
+
 def moe_native(x: torch.Tensor, logits: torch.Tensor, gu: MoeNativeStack, dn: MoeNativeStack, slots: torch.Tensor,
                topk: int, h: torch.Tensor, cs: torch.Tensor | None = None, norm_topk: bool = True,
-               stream=None) -> torch.Tensor:
+               fused: bool = True, stream=None) -> torch.Tensor:
     """The native MoE MLP in the reference's order (src/engine.mm:965-1059): route, gate_up
-    product with the gather fused, SwiGLU with the down matrix's column scale cs, down
-    product, combine into h. x is already times gate_up's column scale."""
+    product with the gather fused, SwiGLU with the down matrix's column scale cs (folded
+    into the gate_up launch when fused), down product, combine into h. x is already times
+    gate_up's column scale."""
     E = slots.numel() - 1
     if gu.Ne % 2 or dn.K != gu.Ne // 2 or dn.Ne != gu.K:
         raise ValueError("gate_up [2I][H] and down [H][I] stacks do not match")
     r = moe_route(logits, E, topk, norm_topk, stream=stream)
-    g = moe_linear_native(x, gu, slots, r, True, stream=stream)
-    act = moe_swiglu(g, gu.Ne // 2, cs, stream=stream)
+    if fused:
+        act = moe_gate_up_native(x, gu, slots, r, cs, stream=stream)
+    else:
+        act = moe_swiglu(moe_linear_native(x, gu, slots, r, True, stream=stream), gu.Ne // 2, cs, stream=stream)
     y = moe_linear_native(act, dn, slots, r, False, stream=stream)
     return moe_combine(y, r, h, stream=stream)

@@ -145,3 +145,28 @@ def test_native_layer_matches_oracle(gpu, book, T, E, topk, H, I):
     ops.moe_native(to_dev(x[:1], gpu), to_dev(logits[:1], gpu), gu, dn, sl, topk, h1, cs=to_dev(cs, gpu))
     _sync()
     assert torch.equal(h1, h[:1])
+
+
+@pytest.mark.parametrize("book", ["int15", "fp4"])
+@pytest.mark.parametrize("H,I", [(512, 256), (4096, 64)])
+def test_native_gate_up_fused_equals_two_launches(gpu, book, H, I):
+    """rlq_moe_gate_up_native gives the bits of the gate/up product followed by the SwiGLU,
+    with and without a column scale."""
+    import torch
+
+    from raceline_amd import ops
+
+    rng = np.random.default_rng(H + I)
+    E, T, topk = 16, 9, 4
+    codes, s_row = make_stack(rng, E + 1, 2 * I, H, book)
+    slots = shuffled_slots(rng, E, 1)
+    c2, s2 = place(codes, s_row, slots, 2 * I, E + 2)
+    st = upload_stack(c2, s2, 2 * I, book, gpu)
+    r = ops.moe_route(to_dev(rng.standard_normal((T, E + 1), dtype=np.float32), gpu), E, topk)
+    x = to_dev(rng.standard_normal((T, H)).astype(np.float16), gpu)
+    sl = to_dev(slots, gpu)
+    for cs in (None, to_dev(rng.uniform(0.5, 1.5, size=I).astype(np.float32), gpu)):
+        fused = ops.moe_gate_up_native(x, st, sl, r, cs)
+        two = ops.moe_swiglu(ops.moe_linear_native(x, st, sl, r, True), I, cs)
+        _sync()
+        assert torch.equal(fused, two)

@@ -249,6 +249,19 @@ int rlq_moe_gate_up_native(const void *x, int x_stride, int T, const int *tok, i
                            const int *n_items, int max_items, const float *cs, void *act, int act_stride,
                            void *stream);
 
+/* The whole native MoE MLP in one call (Engine::encode_moe, src/engine.mm:965-1059, for
+ * native files): route, gate/up with the gather and the SwiGLU, down, combine into h (fp32
+ * [T][h_stride], accumulated). Stacks as for rlq_moe_gate_up_native (gate_up: n_slots
+ * slots of 2I rows, K = H) and rlq_moe_linear_native (down: n_slots slots of H rows,
+ * K = I); slots [E+1]; cs the down matrix's column scale or NULL. The workspace is the
+ * one rlq_moe_workspace_bytes(T, E, topk, H, I) sizes (256-byte aligned, no
+ * initialisation). Up to four tokens the down product and the combine run as one launch,
+ * with the same bits as the step-by-step entry points. */
+int rlq_moe_native(const void *x, int x_stride, const float *logits, int logit_stride, int T, int E, int topk,
+                   int norm_topk, int H, int I, const void *packed_gu, const float *s_gu, const void *packed_dn,
+                   const float *s_dn, const int *slots, int n_slots, int book, const float *cs, float *h,
+                   int h_stride, void *workspace, size_t workspace_bytes, void *stream);
+
 /* act[r][i] = half(silu(gu[r][i]) * gu[r][I + i] * cs[i]) for r < A, i < I: the SwiGLU of
  * kernels/ops.metal:446-455 between the native gate_up and down products. cs is the down
  * matrix's column scale (fp32 [I]; NULL means ones, as for affine matrices). gu fp32

@@ -646,9 +646,13 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
 // the workgroup then adds each token's S slots into its residual row in slot order, with
 // moe_combine_kernel's fused multiply-adds. Same bits as the two launches, without the
 // second one and without writing y. LDS: [A rows][16] floats, then inv [A] and w [A].
-template <int GPW, int SD>
+// BOOK: kAffine, or a native book (int15, fp4) whose expert e sits at slot slots[e] with row
+// scales s_row (the products are then moe_native_kernel's, scaled at the row as there; a
+// slot outside [0, n_slots) contributes zero rows).
+template <int GPW, int SD, int BOOK = kAffine>
 __global__ __launch_bounds__(1024) void moe_down_combine_kernel(MoeArgs a, const int *inv, const float *w, int T,
-                                                                int S, float *h, int h_stride) {
+                                                                int S, float *h, int h_stride, const float *s_row,
+                                                                const int *slots, int n_slots) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   float *ys = reinterpret_cast<float *>(lds);
   const int A = T * S;
@@ -676,15 +680,25 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(MoeArgs a, const
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, xrange);
   for (int item = wave; item < n_items; item += waves) {
     const int4 it = item == wave ? it0 : a.items[item];
-    const int e = it.x, r0 = it.y, rows = it.z;
-    const WaveTile wt = wave_tile(a.codes, a.sb, e * a.tiles_per_expert + tile, G4, 0, GPW);
+    int e = it.x;
+    const int r0 = it.y, rows = it.z;
+    bool ok = true;
+    float sn = 1.0f;
+    if constexpr (BOOK != kAffine) {
+      const int slot = __builtin_amdgcn_readfirstlane(slots[e]);
+      ok = slot >= 0 && slot < n_slots;
+      e = ok ? slot : 0;
+      sn = ok ? s_row[(size_t)e * a.tiles_per_expert * 16 + 16 * tile + c16] : 0.0f;
+    }
+    const WaveTile wt = wave_tile(a.codes, BOOK == kAffine ? a.sb : a.codes, e * a.tiles_per_expert + tile, G4, 0,
+                                  ok ? GPW : 0);
     const bool live = c16 < rows;
     const int xrow = r0 + (live ? c16 : 0);
-    const f32x4 acc = tile_dot_rows<GPW, SD>(wt, rx, (uint32_t)xrow * a.x_stride * 2u + 16u * j4, live, wn, lane);
+    const f32x4 acc = tile_dot_rows<GPW, SD, BOOK>(wt, rx, (uint32_t)xrow * a.x_stride * 2u + 16u * j4, live, wn, lane);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int r = 4 * j4 + v;
-      if (r < rows) ys[(size_t)(r0 + r) * 16 + c16] = acc[v];
+      if (r < rows) ys[(size_t)(r0 + r) * 16 + c16] = BOOK == kAffine ? acc[v] : ok ? sn * acc[v] : 0.0f;
     }
   }
   int *inv_l = reinterpret_cast<int *>(ys + (size_t)A * 16);
@@ -1228,9 +1242,11 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
     const int waves = (int)std::min<size_t>(std::min<size_t>(16, A), moe_max_items(T, E, topk));
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (scale_dtype == RLQ_F16)
-      moe_down_combine_kernel<8, 0><<<H / 16, 64 * waves, A * 72, st>>>(a, inv, w, T, topk + 1, h, h_stride);
+      moe_down_combine_kernel<8, 0><<<H / 16, 64 * waves, A * 72, st>>>(a, inv, w, T, topk + 1, h, h_stride,
+                                                                           nullptr, nullptr, 0);
     else
-      moe_down_combine_kernel<8, 1><<<H / 16, 64 * waves, A * 72, st>>>(a, inv, w, T, topk + 1, h, h_stride);
+      moe_down_combine_kernel<8, 1><<<H / 16, 64 * waves, A * 72, st>>>(a, inv, w, T, topk + 1, h, h_stride,
+                                                                           nullptr, nullptr, 0);
     RLQ_HIP(hipGetLastError());
     return 0;
   }
@@ -1340,6 +1356,65 @@ int rlq_moe_gate_up_native(const void *x, int x_stride, int T, const int *tok, i
 #undef RLQ_NATIVE_GU
   RLQ_HIP(hipGetLastError());
   return 0;
+}
+
+
+int rlq_moe_native(const void *x, int x_stride, const float *logits, int logit_stride, int T, int E, int topk,
+                   int norm_topk, int H, int I, const void *packed_gu, const float *s_gu, const void *packed_dn,
+                   const float *s_dn, const int *slots, int n_slots, int book, const float *cs, float *h,
+                   int h_stride, void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace rlq;
+  if (int rc = check_moe_shape("rlq_moe_native", T, E, topk, H, I)) return rc;
+  const size_t need = rlq_moe_workspace_bytes(T, E, topk, H, I);
+  RLQ_REQUIRE(workspace && workspace_bytes >= need,
+              "rlq_moe_native: workspace of %zu bytes is smaller than the %zu this call needs", workspace_bytes, need);
+  RLQ_REQUIRE(aligned(workspace, 256), "rlq_moe_native: workspace must be 256-byte aligned");
+  RLQ_REQUIRE(h && h_stride >= H, "rlq_moe_native: h is null or h_stride=%d < H=%d", h_stride, H);
+  const size_t A = (size_t)T * (topk + 1);
+  char *p = static_cast<char *>(workspace);
+  int *sel = reinterpret_cast<int *>(p);            p += align256(A * 4);
+  float *w = reinterpret_cast<float *>(p);          p += align256(A * 4);
+  int *tok = reinterpret_cast<int *>(p);            p += align256(A * 4);
+  int *inv = reinterpret_cast<int *>(p);            p += align256(A * 4);
+  int *items = reinterpret_cast<int *>(p);          p += align256((size_t)moe_max_items(T, E, topk) * 16);
+  int *n_items = reinterpret_cast<int *>(p);        p += 256;
+  _Float16 *act = reinterpret_cast<_Float16 *>(p);  p += align256(A * I * 2);
+  float *y = reinterpret_cast<float *>(p);
+  const int max_items = moe_max_items(T, E, topk);
+  if (int rc = rlq_moe_route(logits, logit_stride, T, E, topk, norm_topk, sel, w, tok, inv, items, n_items, stream))
+    return rc;
+  if (int rc = rlq_moe_gate_up_native(x, x_stride, T, tok, H, I, packed_gu, s_gu, slots, n_slots, book, items, n_items,
+                                      max_items, cs, act, I, stream))
+    return rc;
+  if (T <= kDownCombineTokens && expert_gpw(I) == 8 && I / kGroup <= 8) {
+    // a few tokens: down and combine in one launch (the same bits as the two below)
+    RLQ_REQUIRE(book == RLQ_BOOK_INT15 || book == RLQ_BOOK_FP4, "rlq_moe_native: book %d", book);
+    RLQ_REQUIRE(packed_dn && s_dn && aligned(packed_dn, 16), "rlq_moe_native: down stack null or misaligned");
+    MoeArgs a = {};
+    a.x = act;
+    a.codes = static_cast<const u32x4 *>(packed_dn);
+    a.sb = a.codes;
+    a.items = reinterpret_cast<const int4 *>(items);
+    a.n_items = n_items;
+    a.x_rows = (int)A;
+    a.x_stride = I;
+    a.K = I;
+    a.tiles_per_expert = H / 16;
+    const int waves = (int)std::min<size_t>(std::min<size_t>(16, A), moe_max_items(T, E, topk));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (book == RLQ_BOOK_INT15)
+      moe_down_combine_kernel<8, 0, kInt15><<<H / 16, 64 * waves, A * 72, st>>>(a, inv, w, T, topk + 1, h, h_stride,
+                                                                                s_dn, slots, n_slots);
+    else
+      moe_down_combine_kernel<8, 0, kFp4><<<H / 16, 64 * waves, A * 72, st>>>(a, inv, w, T, topk + 1, h, h_stride,
+                                                                              s_dn, slots, n_slots);
+    RLQ_HIP(hipGetLastError());
+    return 0;
+  }
+  if (int rc = rlq_moe_linear_native(act, I, (int)A, nullptr, I, H, packed_dn, s_dn, slots, n_slots, book, items,
+                                     n_items, max_items, y, H, stream))
+    return rc;
+  return rlq_moe_combine(y, H, inv, w, T, topk, H, h, h_stride, stream);
 }
 
 }  // extern "C"

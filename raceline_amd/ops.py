@@ -453,14 +453,33 @@ def moe_gate_up_native(x: torch.Tensor, gu: MoeNativeStack, slots: torch.Tensor,
 
 def moe_native(x: torch.Tensor, logits: torch.Tensor, gu: MoeNativeStack, dn: MoeNativeStack, slots: torch.Tensor,
                topk: int, h: torch.Tensor, cs: torch.Tensor | None = None, norm_topk: bool = True,
-               fused: bool = True, stream=None) -> torch.Tensor:
+               fused: bool = True, one_call: bool = True, workspace: torch.Tensor | None = None,
+               stream=None) -> torch.Tensor:
     """The native MoE MLP in the reference's order (src/engine.mm:965-1059): route, gate_up
     product with the gather fused, SwiGLU with the down matrix's column scale cs (folded
     into the gate_up launch when fused), down product, combine into h. x is already times
-    gate_up's column scale."""
+    gate_up's column scale. one_call: rlq_moe_native (the same bits as the steps)."""
     E = slots.numel() - 1
     if gu.Ne % 2 or dn.K != gu.Ne // 2 or dn.Ne != gu.K:
         raise ValueError("gate_up [2I][H] and down [H][I] stacks do not match")
+    if gu.book != dn.book:
+        raise ValueError("gate_up and down stacks use different codebooks")
+    if one_call:
+        T, H, I = x.shape[0], gu.K, gu.Ne // 2
+        if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < H:
+            raise ValueError("x must be a row-major float16 [T][>= H] matrix")
+        if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+            raise ValueError("logits must be a row-major float32 matrix")
+        if slots.dtype != torch.int32 or not slots.is_contiguous():
+            raise ValueError("slots must be a contiguous int32 vector [E+1]")
+        nbytes = moe_workspace_bytes(T, E, topk, H, I)
+        if workspace is None:
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        lib.call("rlq_moe_native", _ptr(x), x.stride(0), _ptr(logits), logits.stride(0), T, E, topk,
+                 1 if norm_topk else 0, H, I, _ptr(gu.packed), _ptr(gu.s_row), _ptr(dn.packed), _ptr(dn.s_row),
+                 _ptr(slots), gu.n_slots, gu.code, _ptr(cs) if cs is not None else 0, _ptr(h), h.stride(0),
+                 _ptr(workspace), workspace.numel(), _stream(stream))
+        return h
     r = moe_route(logits, E, topk, norm_topk, stream=stream)
     if fused:
         act = moe_gate_up_native(x, gu, slots, r, cs, stream=stream)

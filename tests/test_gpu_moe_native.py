@@ -170,3 +170,29 @@ def test_native_gate_up_fused_equals_two_launches(gpu, book, H, I):
         two = ops.moe_swiglu(ops.moe_linear_native(x, st, sl, r, True), I, cs)
         _sync()
         assert torch.equal(fused, two)
+
+
+@pytest.mark.parametrize("T", [1, 3, 4, 5, 40])
+def test_native_one_call_equals_steps(gpu, T):
+    """rlq_moe_native (down and combine in one launch up to four tokens) gives the bits of
+    the step-by-step entry points."""
+    import torch
+
+    from raceline_amd import ops
+
+    rng = np.random.default_rng(T + 70)
+    E, topk, H, I = 32, 8, 512, 512
+    gq, gs = make_stack(rng, E + 2, 2 * I, H, "fp4")
+    dq, ds = make_stack(rng, E + 2, H, I, "fp4")
+    gu = upload_stack(gq, gs, 2 * I, "fp4", gpu)
+    dn = upload_stack(dq, ds, H, "fp4", gpu)
+    slots = to_dev(shuffled_slots(rng, E, 1), gpu)
+    cs = to_dev(rng.uniform(0.5, 1.5, size=I).astype(np.float32), gpu)
+    x = to_dev(rng.standard_normal((T, H)).astype(np.float16), gpu)
+    logits = to_dev(rng.standard_normal((T, E + 1), dtype=np.float32), gpu)
+    h0 = rng.standard_normal((T, H)).astype(np.float32)
+    h1, h2 = to_dev(h0, gpu), to_dev(h0, gpu)
+    ops.moe_native(x, logits, gu, dn, slots, topk, h1, cs=cs)
+    ops.moe_native(x, logits, gu, dn, slots, topk, h2, cs=cs, one_call=False)
+    _sync()
+    assert torch.equal(h1, h2)

@@ -998,20 +998,13 @@ static void launch_native_inst(dim3 grid, int threads, bool gather, hipStream_t 
 // with the products and the order of moe_native_kernel followed by moe_swiglu_kernel, so
 // the bits are the two launches' without the fp32 gate/up rows in between. The gather is
 // fused (rows are read through tok).
-template <int GPW, int BOOK>
-__global__ __launch_bounds__(1024) void moe_native_gate_up_kernel(const _Float16 *x, int x_stride, int T,
-                                                                  const int *tok, int H, int I, const u32x4 *codes,
-                                                                  const float *s, const int *slots, int n_slots,
-                                                                  const int4 *items, const int *n_items_p,
-                                                                  const float *cs, _Float16 *act, int act_stride) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  const int item = blockIdx.y;
-  const int4 it = items[item];
-  const int n_items = *n_items_p;
-  asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
-  if (item >= n_items) return;                  // uniform: the whole workgroup leaves
-  const int r0 = it.y, rows = it.z;
-  const int slot = __builtin_amdgcn_readfirstlane(slots[it.x]);
+// One workgroup's part: slot `slot`, rows r0 .. r0 + rows - 1 (token tok[r], or token 0
+// when ONE_TOKEN), gate tile blockIdx.x. LDS: the two tiles' reductions, 2 (waves-1) KB.
+template <int GPW, int BOOK, bool ONE_TOKEN>
+__device__ __forceinline__ void native_gate_up_tile(const _Float16 *x, int x_stride, int T, const int *tok, int H,
+                                                    int I, const u32x4 *codes, const float *s, int slot, int n_slots,
+                                                    int r0, int rows, const float *cs, _Float16 *act, int act_stride,
+                                                    unsigned char *lds) {
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1034,7 +1027,7 @@ __global__ __launch_bounds__(1024) void moe_native_gate_up_kernel(const _Float16
   const WaveTile wgt = wave_tile(codes, codes, tg, G4, wg0, GPW);
   const WaveTile wut = wave_tile(codes, codes, tg + I / 16, G4, wg0, GPW);
   const bool live = c16 < rows;
-  const int xrow = min(max(tok[r0 + (live ? c16 : 0)], 0), T - 1);
+  const int xrow = ONE_TOKEN ? 0 : min(max(tok[r0 + (live ? c16 : 0)], 0), T - 1);
   const uint32_t xrange = wn > 0 ? (uint32_t)((T - 1) * x_stride + wn * kGroup) * 2u : 0u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)min(wg0, G) * kGroup, xrange);
   f32x4 ag, au;
@@ -1062,6 +1055,100 @@ __global__ __launch_bounds__(1024) void moe_native_gate_up_kernel(const _Float16
       const float z = silu(sg * ag[v]) * (su * au[v]);
       act[(size_t)(r0 + 4 * j4 + v) * act_stride + n] = static_cast<_Float16>(cs ? z * cs[n] : z);
     }
+}
+
+template <int GPW, int BOOK>
+__global__ __launch_bounds__(1024) void moe_native_gate_up_kernel(const _Float16 *x, int x_stride, int T,
+                                                                  const int *tok, int H, int I, const u32x4 *codes,
+                                                                  const float *s, const int *slots, int n_slots,
+                                                                  const int4 *items, const int *n_items_p,
+                                                                  const float *cs, _Float16 *act, int act_stride) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int item = blockIdx.y;
+  const int4 it = items[item];
+  const int n_items = *n_items_p;
+  asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
+  if (item >= n_items) return;                  // uniform: the whole workgroup leaves
+  const int slot = __builtin_amdgcn_readfirstlane(slots[it.x]);
+  native_gate_up_tile<GPW, BOOK, false>(x, x_stride, T, tok, H, I, codes, s, slot, n_slots, it.y, it.z, cs, act,
+                                        act_stride, lds);
+}
+
+// One token: the routing inside the native gate/up launch, as moe_gate_up_one_token_kernel
+// does for affine experts (wave 0 picks the token's experts; item i is the i-th smallest
+// chosen expert, at row i; workgroup (0, 0) writes the routing tables). LDS: the
+// reductions, then sel [S], w [S] and the chosen experts in ascending order [S].
+template <int GPW, int BOOK, int EPL>
+__global__ __launch_bounds__(1024) void moe_native_gate_up_one_token_kernel(
+    const _Float16 *x, int x_stride, int H, int I, const u32x4 *codes, const float *s, const int *slots, int n_slots,
+    const float *cs, _Float16 *act, int act_stride, const float *logits, int E, int topk, int norm_topk, int *sel,
+    float *w, int *tok, int *inv, int4 *items, int *n_items) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int S = topk + 1;
+  const int waves = blockDim.x >> 6;
+  int *sel_l = reinterpret_cast<int *>(lds + (size_t)2 * (waves - 1) * 64 * 16);
+  float *w_l = reinterpret_cast<float *>(sel_l + S);
+  int *order = reinterpret_cast<int *>(w_l + S);
+  if (threadIdx.x < 64) topk_token<EPL>(logits, E, topk, norm_topk, sel_l, w_l, threadIdx.x);
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < S) {
+    const int es = sel_l[t];
+    int rank = 0;
+    for (int q = 0; q < S; ++q) rank += sel_l[q] < es;
+    order[rank] = es;
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      sel[t] = es;
+      w[t] = w_l[t];
+      inv[t] = rank;
+      tok[rank] = 0;
+      items[rank] = int4{es, rank, 1, 0};
+      if (t == 0) *n_items = S;
+    }
+  }
+  __syncthreads();
+  const int i = blockIdx.y;
+  const int slot = __builtin_amdgcn_readfirstlane(slots[order[i]]);
+  native_gate_up_tile<GPW, BOOK, true>(x, x_stride, 1, nullptr, H, I, codes, s, slot, n_slots, i, 1, cs, act,
+                                       act_stride, lds);
+}
+
+template <int GPW, int BOOK, int EPL>
+static void launch_native_one_token_inst(int S, hipStream_t st, const _Float16 *x, int x_stride, int H, int I,
+                                         const u32x4 *codes, const float *s, const int *slots, int n_slots,
+                                         const float *cs, _Float16 *act, int act_stride, const float *logits, int E,
+                                         int topk, int norm_topk, int *sel, float *w, int *tok, int *inv, int4 *items,
+                                         int *n_items) {
+  const int waves = expert_waves(H);
+  const size_t lds = (size_t)2 * (waves - 1) * 64 * 16 + (size_t)S * 12;
+  moe_native_gate_up_one_token_kernel<GPW, BOOK, EPL><<<dim3(I / 16, S), 64 * waves, lds, st>>>(
+      x, x_stride, H, I, codes, s, slots, n_slots, cs, act, act_stride, logits, E, topk, norm_topk, sel, w, tok, inv,
+      items, n_items);
+}
+
+// Routing and the native gate/up + SwiGLU of one token in one launch; returns 1 when the
+// shape has no such kernel (E > 256 or more than 16 groups per wave).
+static int native_one_token(int book, const _Float16 *x, int x_stride, int H, int I, const u32x4 *codes,
+                            const float *s, const int *slots, int n_slots, const float *cs, _Float16 *act,
+                            const float *logits, int E, int topk, int norm_topk, int *sel, float *w, int *tok,
+                            int *inv, int4 *items, int *n_items, hipStream_t st) {
+  const int epl = (E + 63) / 64, gpw = expert_gpw(H), S = topk + 1;
+  if (epl > 4 || (gpw != 8 && gpw != 16)) return 1;
+#define RLQ_NOT(G, B, P)                                                                                           \
+  launch_native_one_token_inst<G, B, P>(S, st, x, x_stride, H, I, codes, s, slots, n_slots, cs, act, I, logits, E, \
+                                        topk, norm_topk, sel, w, tok, inv, items, n_items)
+#define RLQ_NOT_EPL(G, B) (epl <= 1 ? RLQ_NOT(G, B, 1) : epl <= 2 ? RLQ_NOT(G, B, 2) : RLQ_NOT(G, B, 4))
+  if (book == RLQ_BOOK_INT15) {
+    if (gpw == 8) RLQ_NOT_EPL(8, kInt15);
+    else RLQ_NOT_EPL(16, kInt15);
+  } else {
+    if (gpw == 8) RLQ_NOT_EPL(8, kFp4);
+    else RLQ_NOT_EPL(16, kFp4);
+  }
+#undef RLQ_NOT_EPL
+#undef RLQ_NOT
+  RLQ_HIP(hipGetLastError());
+  return 0;
 }
 
 template <int GPW, int BOOK>
@@ -1381,11 +1468,26 @@ int rlq_moe_native(const void *x, int x_stride, const float *logits, int logit_s
   _Float16 *act = reinterpret_cast<_Float16 *>(p);  p += align256(A * I * 2);
   float *y = reinterpret_cast<float *>(p);
   const int max_items = moe_max_items(T, E, topk);
-  if (int rc = rlq_moe_route(logits, logit_stride, T, E, topk, norm_topk, sel, w, tok, inv, items, n_items, stream))
-    return rc;
-  if (int rc = rlq_moe_gate_up_native(x, x_stride, T, tok, H, I, packed_gu, s_gu, slots, n_slots, book, items, n_items,
-                                      max_items, cs, act, I, stream))
-    return rc;
+  int separate = 1;
+  if (T == 1) {
+    // one token: routing inside the gate/up launch where a kernel covers the shape
+    RLQ_REQUIRE(book == RLQ_BOOK_INT15 || book == RLQ_BOOK_FP4, "rlq_moe_native: book %d (int15 or fp4)", book);
+    RLQ_REQUIRE(x && logits && logit_stride >= E + 1 && packed_gu && s_gu && slots && x_stride >= H &&
+                    x_stride % 8 == 0 && aligned(x, 16) && aligned(packed_gu, 16) && n_slots >= 1 && I % 16 == 0,
+                "rlq_moe_native: bad one-token arguments");
+    separate = native_one_token(book, static_cast<const _Float16 *>(x), x_stride, H, I,
+                                static_cast<const u32x4 *>(packed_gu), s_gu, slots, n_slots, cs, act, logits, E,
+                                topk, norm_topk, sel, w, tok, inv, reinterpret_cast<int4 *>(items), n_items,
+                                static_cast<hipStream_t>(stream));
+    if (separate < 0) return separate;
+  }
+  if (separate) {
+    if (int rc = rlq_moe_route(logits, logit_stride, T, E, topk, norm_topk, sel, w, tok, inv, items, n_items, stream))
+      return rc;
+    if (int rc = rlq_moe_gate_up_native(x, x_stride, T, tok, H, I, packed_gu, s_gu, slots, n_slots, book, items,
+                                        n_items, max_items, cs, act, I, stream))
+      return rc;
+  }
   if (T <= kDownCombineTokens && expert_gpw(I) == 8 && I / kGroup <= 8) {
     // a few tokens: down and combine in one launch (the same bits as the two below)
     RLQ_REQUIRE(book == RLQ_BOOK_INT15 || book == RLQ_BOOK_FP4, "rlq_moe_native: book %d", book);

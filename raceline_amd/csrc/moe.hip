@@ -398,6 +398,9 @@ struct MoeArgs {
   void *out;                // gate_up: act fp16 [A][out_stride]; down: y fp32 [A][out_stride]
   int x_rows, x_stride, K, tiles_per_expert, out_stride;
   int tiles_per_block, waves_per_tile;   // the staged kernel's workgroup shape
+  const float *s_row;       // native books: row scales of the slots; slots[e]: expert e's slot
+  const int *slots;
+  int n_slots;
 };
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
@@ -518,9 +521,13 @@ __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, 
 // sums are the per-tile kernel's. Up to K = 2048 (CPL <= 4) the kernel is held to 80 VGPRs (six
 // waves per SIMD), which lets two 12-wave workgroups share a CU; at K = 4096 LDS allows one
 // workgroup per CU and the registers are left free.
-template <int GPW, int SD, int KIND, int CPL, int SUB>
+// BOOK: kAffine, or (KIND 1 only) a native book: expert e's matrix sits at slot
+// a.slots[e] with row scales a.s_row, the products chain as moe_native_kernel's do and the
+// row scale is applied at the store (a slot outside the table gives zero rows).
+template <int GPW, int SD, int KIND, int CPL, int SUB, int BOOK = kAffine>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 6 : 1))) void moe_expert_lds_kernel(
     MoeArgs a) {
+  static_assert(BOOK == kAffine || KIND == 1, "native books: the down kind only");
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int item = blockIdx.y;
   // the item entry is read together with the count (the list holds the most items a call
@@ -529,7 +536,14 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
   const int n_items = *a.n_items;
   asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
   if (item >= n_items) return;                  // uniform: the whole workgroup leaves
-  const int e = it.x, r0 = it.y, rows = it.z;
+  int e = it.x;
+  const int r0 = it.y, rows = it.z;
+  bool slot_ok = true;
+  if constexpr (BOOK != kAffine) {
+    const int slot = __builtin_amdgcn_readfirstlane(a.slots[e]);
+    slot_ok = slot >= 0 && slot < a.n_slots;    // uniform; a bad slot reads slot 0, writes zeros
+    e = slot_ok ? slot : 0;
+  }
   const int tid = threadIdx.x, nthreads = blockDim.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -565,15 +579,15 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = lane + 64 * j;
-      if (c < cpr) *reinterpret_cast<u32x4 *>(xs + (size_t)row * rstride + 8 * c) = prep_x8(xr[j]);
+      if (c < cpr) *reinterpret_cast<u32x4 *>(xs + (size_t)row * rstride + 8 * c) = prep_act<BOOK>(xr[j]);
     }
   };
   u32x4 xr[CPL];
   load_row(wave, xr);
   // 2. every weight load of this wave's part of its tile
   u32x4 wq[GPW / 2], sq[GPW / 4];
-  const WaveTile wt = wave_tile(a.codes, a.sb, t, G4, wg0, wn > 0 ? GPW : 0);
-  issue_tile_loads<GPW>(wt, lane, wq, sq);
+  const WaveTile wt = wave_tile(a.codes, BOOK == kAffine ? a.sb : a.codes, t, G4, wg0, wn > 0 ? GPW : 0);
+  issue_tile_loads<GPW, BOOK>(wt, lane, wq, sq);
   __builtin_amdgcn_sched_barrier(0);
   // 3. rows -> LDS in operand order (loads complete in issue order: the first row waits
   // for its own loads only); a workgroup of fewer than 16 waves stages the rest in turn
@@ -584,7 +598,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
   }
   __syncthreads();
   // 4. the group sums of the 16 rows, once for every tile: wave w forms groups w, w + nw, ...
-  for (int g = wave; g < G; g += nw) {
+  for (int g = wave; BOOK == kAffine && g < G; g += nw) {
     const _Float16 *xa = xs + (size_t)c16 * rstride + 8 * j4 + (size_t)g * kGroup;
     half8 af[2];
 #pragma unroll
@@ -595,7 +609,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
   __syncthreads();
   // 5. products, then the sub-parts of each tile meet in order (only those with groups)
   f32x4 accs[SUB];
-  tile_dot_lds<GPW, SD, SUB>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn, lane, accs);
+  tile_dot_lds<GPW, SD, SUB, BOOK>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn, lane, accs);
   constexpr int per = GPW / SUB;
   if (part > 0) {
 #pragma unroll
@@ -631,10 +645,14 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
     }
   } else {
     float *y = static_cast<float *>(a.out);
+    float sn = 1.0f;
+    if constexpr (BOOK != kAffine) sn = a.s_row[(size_t)e * a.tiles_per_expert * 16 + 16 * tile + c16];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int r = 4 * j4 + v;
-      if (r < rows) y[(size_t)(r0 + r) * a.out_stride + 16 * tile + c16] = acc[v];
+      if (r < rows)
+        y[(size_t)(r0 + r) * a.out_stride + 16 * tile + c16] =
+            BOOK == kAffine ? acc[v] : slot_ok ? sn * acc[v] : 0.0f;
     }
   }
 }
@@ -780,7 +798,7 @@ static int staged_waves(int gpw, int W, int sub, size_t lds_rows) {
   return gpw == 16 && 2 * lds12 <= kMaxLdsBytes ? 12 : 16;
 }
 
-template <int GPW, int SD, int KIND, int SUB>
+template <int GPW, int SD, int KIND, int SUB, int BOOK = kAffine>
 static int launch_staged_inst(int tpe, hipStream_t st, MoeArgs a, int items) {
   const int G = a.K / kGroup, W = (G + GPW - 1) / GPW;
   const size_t lds_rows = (size_t)16 * (a.K + 8) * 2 + (size_t)G * 16 * 4;
@@ -792,17 +810,17 @@ static int launch_staged_inst(int tpe, hipStream_t st, MoeArgs a, int items) {
   const size_t lds = lds_rows + (size_t)tpb * (W - 1) * SUB * 64 * 16;
   const dim3 grid((tpe + tpb - 1) / tpb, items);
   static LdsOptIn lds_opt[4];
-  const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB>)};
+  const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK>)};
   const int which = xpt <= 1 ? 0 : xpt <= 2 ? 1 : xpt <= 4 ? 2 : 3;
   if (xpt <= 8)
     if (int rc = allow_large_lds(fns[which], lds_opt[which])) return rc;
-  if (xpt <= 1) moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 2) moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 4) moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 8) moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB><<<grid, threads, lds, st>>>(a);
+  if (xpt <= 1) moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 2) moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 4) moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 8) moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK><<<grid, threads, lds, st>>>(a);
   else return fail("moe: %d activation chunks per thread (K=%d) is more than the staged kernel takes", xpt, a.K);
   RLQ_HIP(hipGetLastError());
   return 0;
@@ -1370,6 +1388,37 @@ int rlq_moe_linear_native(const void *a, int a_stride, int a_rows, const int *to
   auto codes = static_cast<const u32x4 *>(packed);
   auto it = reinterpret_cast<const int4 *>(items);
   const bool gather = tok != nullptr;
+  if (!gather && K <= kStagedMaxK && a_rows >= 64) {
+    // sorted rows in bulk (the down kind of a batch): the staged kernel, whose sub-parts
+    // give the per-tile kernel's sums, so the choice does not change a row's bits
+    MoeArgs m = {};
+    m.x = ah;
+    m.codes = codes;
+    m.sb = codes;
+    m.items = it;
+    m.n_items = n_items;
+    m.out = c;
+    m.x_rows = a_rows;
+    m.x_stride = a_stride;
+    m.K = K;
+    m.tiles_per_expert = Ne / 16;
+    m.out_stride = c_stride;
+    m.s_row = s;
+    m.slots = slots;
+    m.n_slots = n_slots;
+    const int sub = staged_gpw(K) / expert_gpw(K);
+    int rc;
+    if (staged_gpw(K) == 8)
+      rc = book == RLQ_BOOK_INT15 ? launch_staged_inst<8, 0, 1, 1, kInt15>(Ne / 16, st, m, max_items)
+                                  : launch_staged_inst<8, 0, 1, 1, kFp4>(Ne / 16, st, m, max_items);
+    else if (sub == 2)
+      rc = book == RLQ_BOOK_INT15 ? launch_staged_inst<16, 0, 1, 2, kInt15>(Ne / 16, st, m, max_items)
+                                  : launch_staged_inst<16, 0, 1, 2, kFp4>(Ne / 16, st, m, max_items);
+    else
+      rc = book == RLQ_BOOK_INT15 ? launch_staged_inst<16, 0, 1, 1, kInt15>(Ne / 16, st, m, max_items)
+                                  : launch_staged_inst<16, 0, 1, 1, kFp4>(Ne / 16, st, m, max_items);
+    return rc;
+  }
 #define RLQ_NATIVE(G, B) \
   launch_native_inst<G, B>(grid, threads, gather, st, ah, a_stride, a_rows, tok, K, Ne, codes, s, slots, n_slots, it, \
                            n_items, c, c_stride)

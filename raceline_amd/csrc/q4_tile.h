@@ -477,7 +477,9 @@ __device__ __forceinline__ f32x4 tile_dot_rows_staged(const WaveTile &w, __amdgp
 // Lane (c16, j4) reads row c16. The part is summed as SUB consecutive sub-parts of GPW / SUB
 // groups, each in its own accumulator (acc[s], from zero), which is how a kernel with
 // GPW / SUB groups per wave sums the same groups.
-template <int GPW, int SD, int SUB>
+// BOOK: kAffine, or a native book (int15, fp4), whose products chain in the MFMA over each
+// sub-part (no per-group scale or group sums; gs unused), as tile_dot_rows chains them.
+template <int GPW, int SD, int SUB, int BOOK = kAffine>
 __device__ __forceinline__ void tile_dot_lds(const u32x4 (&wq)[GPW / 2], const u32x4 (&sq)[GPW / 4],
                                              const _Float16 *xs, const float *gs, int rstride, int wn, int lane,
                                              f32x4 (&acc)[SUB]) {
@@ -492,8 +494,15 @@ __device__ __forceinline__ void tile_dot_lds(const u32x4 (&wq)[GPW / 2], const u
       half8 af[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(xa + jg * kGroup + 32 * s);
-      const f32x4 gsv = *reinterpret_cast<const f32x4 *>(ga + 16 * jg);
-      group_step_gs<GPW, SD, 4>(acc[jg / per], af, gsv, wq, sq, jg);
+      if constexpr (BOOK == kAffine) {
+        const f32x4 gsv = *reinterpret_cast<const f32x4 *>(ga + 16 * jg);
+        group_step_gs<GPW, SD, 4>(acc[jg / per], af, gsv, wq, sq, jg);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          acc[jg / per] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              af[s], native8_to_half8<BOOK>(wq[jg >> 1][2 * (jg & 1) + s]), acc[jg / per], 0, 0, 0);
+      }
       asm volatile("" : "+v"(acc[jg / per]));
     }
   }

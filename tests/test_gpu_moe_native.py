@@ -55,12 +55,14 @@ def place(codes, s_row, slots, Ne, n_slots):
 
 
 @pytest.mark.parametrize("book", ["int15", "fp4"])
-@pytest.mark.parametrize("gather,K,Ne", [(True, 512, 256), (False, 256, 512), (True, 4096, 64), (False, 9216, 48)])
-def test_native_expert_linear(gpu, book, gather, K, Ne):
+@pytest.mark.parametrize("gather,K,Ne,T", [(True, 512, 256, 11), (False, 256, 512, 11), (True, 4096, 64, 11),
+                                          (False, 9216, 48, 11), (False, 512, 256, 20), (False, 2048, 64, 20)])
+def test_native_expert_linear(gpu, book, gather, K, Ne, T):
+    """(the last two: sorted rows in bulk, the staged kernel; K = 2048 sums in sub-parts)"""
     from raceline_amd import ops
 
-    rng = np.random.default_rng(K + Ne + (7 if gather else 0))
-    E, T, topk = 16, 11, 4
+    rng = np.random.default_rng(K + Ne + T + (7 if gather else 0))
+    E, topk = 16, 4
     S = topk + 1
     codes, s_row = make_stack(rng, E + 1, Ne, K, book)
     slots = shuffled_slots(rng, E, 3)
@@ -116,8 +118,11 @@ def test_native_int16_is_refused(gpu):
 
 
 @pytest.mark.parametrize("book", ["int15", "fp4"])
-@pytest.mark.parametrize("T,E,topk,H,I", [(1, 16, 4, 256, 128), (6, 64, 8, 512, 256), (40, 32, 4, 256, 512)])
+@pytest.mark.parametrize("T,E,topk,H,I", [(1, 16, 4, 256, 128), (6, 64, 8, 512, 256), (40, 32, 4, 256, 512),
+                                           (20, 16, 4, 256, 2048)])
 def test_native_layer_matches_oracle(gpu, book, T, E, topk, H, I):
+    """(T = 20 and 40: the down product of the batch runs on the staged kernel, the token
+    alone on the per-tile or the down + combine kernel: the bits must agree)"""
     import torch
 
     from raceline_amd import ops

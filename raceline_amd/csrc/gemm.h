@@ -10,9 +10,10 @@ struct GemmArgs {
   const _Float16 *x;    // affine: the prepped activations [M][K]; native: x [M][x_stride]
   const u32x4 *codes;
   const u32x4 *sb;      // affine: scale/bias quads
-  const _Float16 *gshl; // affine: group sums as fp16 (hi, lo) pairs [M][gs_stride]
+  const uint16_t *gs;   // affine: the group sums' pieces, fp16 or bf16 bits [M][gs_stride]
   const float *srow;    // native books: row scales [N]
   const float *asum;    // kInt16: activation row sums [M]
+  const float *rscale;  // affine: 2^-e per row, undoing the prep pass's prescale [M]
   float *y;
   float *y_part;        // split K: the second half's partial products [M][y_part_stride]
   int x_stride, M, K, N, y_stride, gs_stride;

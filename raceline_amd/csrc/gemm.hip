@@ -16,8 +16,9 @@
 //  - The 32 MFMAs of a pair run in a fixed order with each A fragment read from LDS 8
 //    MFMAs ahead; affine group products are scaled into the fp32 accumulators by FMAs
 //    interleaved with the MFMAs of the next half-group.
-// Affine: the activations are first rewritten by a prep pass into the operand order of
-// q4_tile.h (x0, x4, x1/16, x5/16, ...), matching the cheap code conversion. The bias term
+// Affine: the activations are first rewritten by a prep pass (exact per-row power-of-two
+// prescale, then the operand order (x0, x4, x1/16, x5/16, ...) of the five-op code
+// conversion), and the outputs are scaled back at the store. The bias term
 // sum_g b[n][g] gsum[m][g] is one more MFMA product at the end, over K' = 2G, with the
 // group sums split into fp16 hi + lo (exact to 2^-22) and b as the other operand.
 // Native books: activations are used as they are, codes decode in element order, and the
@@ -42,34 +43,114 @@ constexpr int kStages = 3;                  // loads run two group pairs ahead o
 
 // ------------------------------------------------------------------ affine prep pass
 
-// xp[m][k]: x in operand order (prep_x8 per 8 elements); gshl[m][2g], [2g+1]: the group
-// sum split into fp16 hi and lo. One thread per 8 activations (coalesced 16-byte loads and
-// stores); the 8 threads of a group add their partial sums with a fixed butterfly.
-__global__ void gemm_prep_kernel(const _Float16 *x, int x_stride, int M, int K, _Float16 *xp, _Float16 *gshl,
-                                 int gs_stride) {
+// The GEMM's code conversion is the five-op form of q4_tile.h (odd codes at 16 times the
+// scale), so the odd activations go in divided by 16. A division by 16 in fp16 rounds
+// values below 2^-10 onto the subnormal grid, which would make the result depend on the
+// activations' scale. So each row is first multiplied by a power of two, 2^e with e chosen
+// from the row's largest magnitude (max |x| 2^e in [2^8, 2^9)), and the GEMM multiplies
+// its outputs by 2^-e: powers of two change no bits in fp32, and after the prescale only
+// elements below 2^-19 of the row's largest one reach the subnormal grid (an error below
+// 2^-29 of that largest element each). 2^8 keeps each group sum of 64 scaled elements
+// within fp16 range for the bias product.
+constexpr int kPrepThreads = 256;
+
+// eight consecutive activations times f (even elements) and f / 16 (odd ones) -> operand
+// order (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16), rounded to fp16 once
+__device__ __forceinline__ u32x4 prep_x8_scaled(u32x4 p, float f) {
+  const half8 h = __builtin_bit_cast(half8, p);
+  const float fo = f * 0.0625f;
+  half8 o;
+  o[0] = (_Float16)((float)h[0] * f);  o[1] = (_Float16)((float)h[4] * f);
+  o[2] = (_Float16)((float)h[1] * fo); o[3] = (_Float16)((float)h[5] * fo);
+  o[4] = (_Float16)((float)h[2] * f);  o[5] = (_Float16)((float)h[6] * f);
+  o[6] = (_Float16)((float)h[3] * fo); o[7] = (_Float16)((float)h[7] * fo);
+  return __builtin_bit_cast(u32x4, o);
+}
+
+// The group sums feed the bias product sum_g b[n][g] gsum[m][g], an MFMA over K' = P G with
+// each group sum split into P exact pieces of the biases' 16-bit type: fp16 biases (SD 0)
+// take (hi, lo), exact to 2^-22 of the sum; bf16 biases (SD 1) take (hi, mid, lo, 0), whose
+// three 8-bit pieces hold the fp32 sum exactly. The bf16 product keeps bf16 biases exact
+// (converting them to fp16 would round those below 2^-14).
+template <int SD> constexpr int kGsPieces = SD == 0 ? 2 : 4;
+static int gs_stride_of(int G, int sd) { return ((sd == 0 ? 2 : 4) * G + 31) / 32 * 32; }
+
+__device__ __forceinline__ uint32_t bf16_rne_bits(float v) {   // finite v
+  const uint32_t u = __float_as_uint(v);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// One workgroup per token row m. Pass 1 finds max |x| of the row; pass 2 writes
+// xp[m][k] (the row times 2^e, in operand order), gs[m][P g ..] (the pieces of the group
+// sums of the scaled row) and rscale[m] = 2^-e. One thread per 8 activations per step
+// (coalesced 16-byte loads and stores); the 8 threads of a group add their partial sums
+// with a fixed butterfly. A row that is all zeros, or holds an infinity or a NaN, keeps
+// e = 0.
+template <int SD>
+__global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(const _Float16 *x, int x_stride, int M, int K,
+                                                                 _Float16 *xp, uint16_t *gs, int gs_stride,
+                                                                 float *rscale) {
+  constexpr int P = kGsPieces<SD>;
+  __shared__ float wmax[kPrepThreads / 64];
+  const int m = blockIdx.x;
   const int C = K / 8;                                  // chunks per row (a multiple of 8)
-  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool in = idx < (long long)M * C;
-  const int m = in ? (int)(idx / C) : 0, c = in ? (int)(idx - (long long)m * C) : 0;
-  u32x4 v = {};
-  if (in) v = *reinterpret_cast<const u32x4 *>(x + (size_t)m * x_stride + 8 * c);
-  const half8 h = __builtin_bit_cast(half8, v);
-  float sum = 0.0f;
+  const _Float16 *row = x + (size_t)m * x_stride;
+  float mx = 0.0f;
+  for (int c = threadIdx.x; c < C; c += kPrepThreads) {
+    const half8 h = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4 *>(row + 8 * c));
 #pragma unroll
-  for (int e = 0; e < 8; ++e) sum += static_cast<float>(h[e]);
-  sum += __shfl_xor(sum, 1);
-  sum += __shfl_xor(sum, 2);
-  sum += __shfl_xor(sum, 4);
-  if (!in) return;
-  *reinterpret_cast<u32x4 *>(xp + (size_t)m * K + 8 * c) = prep_x8(v);
-  if ((c & 7) == 0) {
-    const int g = c >> 3, G = C >> 3;
-    const _Float16 hi = static_cast<_Float16>(sum);
-    const _Float16 lo = static_cast<_Float16>(sum - static_cast<float>(hi));
-    gshl[(size_t)m * gs_stride + 2 * g] = hi;
-    gshl[(size_t)m * gs_stride + 2 * g + 1] = lo;
-    if (g == G - 1)   // the row's padding up to gs_stride is zero (no memset: this runs in graphs)
-      for (int k = 2 * G; k < gs_stride; ++k) gshl[(size_t)m * gs_stride + k] = (_Float16)0.0f;
+    for (int e = 0; e < 8; ++e) mx = __builtin_fmaxf(mx, __builtin_fabsf(static_cast<float>(h[e])));
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, d));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kPrepThreads / 64; ++w) mx = __builtin_fmaxf(mx, wmax[w]);
+  int ex = 0;
+  if (mx > 0.0f && mx <= 65504.0f) {
+    int k;
+    (void)__builtin_frexpf(mx, &k);                     // mx = f 2^k, f in [0.5, 1)
+    ex = 9 - k;                                         // mx 2^ex in [2^8, 2^9)
+  }
+  const float f = __builtin_ldexpf(1.0f, ex);
+  if (threadIdx.x == 0) rscale[m] = __builtin_ldexpf(1.0f, -ex);
+  const int G = C >> 3;
+  for (int c0 = 0; c0 < C; c0 += kPrepThreads) {        // uniform trip count: the butterfly needs every lane
+    const int c = c0 + threadIdx.x;
+    const bool in = c < C;
+    u32x4 v = {};
+    if (in) v = *reinterpret_cast<const u32x4 *>(row + 8 * c);
+    const half8 h = __builtin_bit_cast(half8, v);
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum += static_cast<float>(h[e]) * f;
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    if (!in) continue;
+    *reinterpret_cast<u32x4 *>(xp + (size_t)m * K + 8 * c) = prep_x8_scaled(v, f);
+    if ((c & 7) == 0) {
+      const int g = c >> 3;
+      uint16_t *dst = gs + (size_t)m * gs_stride + P * g;
+      if constexpr (SD == 0) {
+        const _Float16 hi = static_cast<_Float16>(sum);
+        const _Float16 lo = static_cast<_Float16>(sum - static_cast<float>(hi));
+        dst[0] = __builtin_bit_cast(uint16_t, hi);
+        dst[1] = __builtin_bit_cast(uint16_t, lo);
+      } else {
+        const uint32_t hi = bf16_rne_bits(sum);
+        const float r1 = sum - __uint_as_float(hi << 16);         // exact
+        const uint32_t mid = bf16_rne_bits(r1);
+        const uint32_t lo = bf16_rne_bits(r1 - __uint_as_float(mid << 16));   // exact: 8 bits remain
+        dst[0] = (uint16_t)hi;
+        dst[1] = (uint16_t)mid;
+        dst[2] = (uint16_t)lo;
+        dst[3] = 0;
+      }
+      if (g == G - 1)   // the row's padding up to gs_stride is zero (no memset: this runs in graphs)
+        for (int k = P * G; k < gs_stride; ++k) gs[(size_t)m * gs_stride + k] = 0;
+    }
   }
 }
 
@@ -317,40 +398,43 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   }
 
   if (BOOK == kAffine && split == 0) {
-    // acc += sum_g b[n][g] * gsum[m][g]: an MFMA product over K' = 2G, the group sums as
-    // (hi, lo) pairs. Step st covers k' = 16 st .. +15; lane half h holds k' 16 st + 8 h
-    // .. +7, i.e. the (hi, lo) of groups 8 st + 4 h .. +3: b of those groups, each twice.
-    // The scale quads come straight from memory.
+    // acc += sum_g b[n][g] * gsum[m][g]: an MFMA product over K' = P G, each group sum as P
+    // pieces (gemm_prep_kernel). Step st covers k' = 16 st .. +15; lane half h holds k'
+    // 16 st + 8 h .. +7: for fp16 biases (P = 2) the (hi, lo) of groups 8 st + 4 h .. +3, so
+    // b of those groups, each twice; for bf16 biases (P = 4) the pieces of groups
+    // 4 st + 2 h and + 1, so b of those two, four times each. The scale quads come
+    // straight from memory.
     const int tn = t0 + 2 * wave;
     const int tv = max(0, min(T, tn + 2) - tn);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sb + (size_t)min(tn, T) * G4 * 16, (uint32_t)tv * G4 * 256u);
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.gshl, (uint32_t)((size_t)a.M * a.gs_stride * 2));
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.gs, (uint32_t)((size_t)a.M * a.gs_stride * 2));
     const int steps = a.gs_stride / 16;
     for (int st = 0; st < steps; ++st) {
-      const int q = 2 * st + h;                      // quad of groups 4q .. 4q+3
+      const int q = SD == 0 ? 2 * st + h : st;       // quad of groups 4q .. 4q+3
       const u32x4 v = q < G4 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                              rs, (uint32_t)tt * G4 * 256u + (uint32_t)q * 256u + 16u * cr, 0, 0))
                              : u32x4{};
       u32x4 d;
+      if constexpr (SD == 0) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t bbits = v[e] >> 16;
-        uint32_t hb;
-        if constexpr (SD == 0) {
-          hb = bbits;
-        } else {
-          hb = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__uint_as_float(bbits << 16)));
-        }
-        d[e] = hb | (hb << 16);                       // (b, b): times gsum hi and lo
+        for (int e = 0; e < 4; ++e) d[e] = (v[e] >> 16) * 0x10001u;           // (b, b): times hi and lo
+      } else {
+        const uint32_t b0 = (h ? v[2] : v[0]) >> 16, b1 = (h ? v[3] : v[1]) >> 16;
+        d[0] = d[1] = b0 * 0x10001u;                                           // b of group 4q + 2h, four times
+        d[2] = d[3] = b1 * 0x10001u;                                           // and of group 4q + 2h + 1
       }
-      const half8 bb = __builtin_bit_cast(half8, d);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const int m = m0 + mt * 32 + c32;
-        const half8 ag = __builtin_bit_cast(
-            half8, __builtin_amdgcn_raw_buffer_load_b128(
+        const u32x4 ag = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                        rg, m < a.M ? (uint32_t)(((size_t)m * a.gs_stride + 16 * st + 8 * h) * 2) : kFarOffset, 0, 0));
-        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ag, bb, acc[mt], 0, 0, 0);
+        if constexpr (SD == 0)
+          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, ag), __builtin_bit_cast(half8, d),
+                                                          acc[mt], 0, 0, 0);
+        else
+          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ag),
+                                                           __builtin_bit_cast(bf16x8, d), acc[mt], 0, 0, 0);
       }
     }
   }
@@ -366,6 +450,7 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
       const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
       if (m < a.M) {
         float val = acc[mt][v];
+        if constexpr (BOOK == kAffine) val *= a.rscale[m];   // undoes the prep's 2^e, exactly
         if constexpr (BOOK == kInt16) {
           if (split == 0) val = __builtin_fmaf(0.5f, a.asum[m], val);
         }
@@ -387,8 +472,9 @@ static bool split_k(int K, int N) { return K >= 2 * N && (K / kGroup + 1) / 2 >=
 
 static size_t books_workspace(int book, int M, int K) {
   const int G = K / kGroup;
-  const size_t gs_stride = (size_t)(2 * G + 31) / 32 * 32;
-  if (book == kAffine) return ((size_t)M * K * 2 + 255) / 256 * 256 + ((size_t)M * gs_stride * 2 + 255) / 256 * 256;
+  if (book == kAffine)   // the group-sum pieces sized for bf16 biases, the larger of the two
+    return ((size_t)M * K * 2 + 255) / 256 * 256 + ((size_t)M * gs_stride_of(G, 1) * 2 + 255) / 256 * 256 +
+           ((size_t)M * sizeof(float) + 255) / 256 * 256;
   if (book == kInt16) return ((size_t)(G + 1) * ((M + 127) / 128 * 128) * sizeof(float) + 255) / 256 * 256;
   return 0;
 }
@@ -430,13 +516,16 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
   a.y = y;
   a.M = M; a.K = K; a.N = N; a.y_stride = y_stride;
   if (book == kAffine) {
-    const int gs_stride = (2 * G + 31) / 32 * 32;
+    const int gs_stride = gs_stride_of(G, sd);
     _Float16 *xp = static_cast<_Float16 *>(ws);
-    _Float16 *gshl = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + ((size_t)M * K * 2 + 255) / 256 * 256);
-    const long long chunks = (long long)M * (K / 8);
-    gemm_prep_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, st>>>(x, x_stride, M, K, xp, gshl, gs_stride);
+    const size_t xp_bytes = ((size_t)M * K * 2 + 255) / 256 * 256;
+    uint16_t *gs = reinterpret_cast<uint16_t *>(static_cast<char *>(ws) + xp_bytes);
+    float *rscale = reinterpret_cast<float *>(static_cast<char *>(ws) + xp_bytes +
+                                              ((size_t)M * gs_stride_of(G, 1) * 2 + 255) / 256 * 256);
+    if (sd == RLQ_BF16) gemm_prep_kernel<1><<<M, kPrepThreads, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale);
+    else gemm_prep_kernel<0><<<M, kPrepThreads, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale);
     RLQ_HIP(hipGetLastError());
-    a.x = xp; a.x_stride = K; a.gshl = gshl; a.gs_stride = gs_stride;
+    a.x = xp; a.x_stride = K; a.gs = gs; a.gs_stride = gs_stride; a.rscale = rscale;
   } else {
     a.x = x; a.x_stride = x_stride;
     if (book == kInt16) {

@@ -203,6 +203,10 @@ static int gemv_gpw(int K) {
   return g <= 8 * 16 ? 8 : g <= 12 * 16 ? 12 : g <= 16 * 16 ? 16 : 24;
 }
 static int gemv_waves(int K) { const int g = gemv_gpw(K); return (4 * quads_of(K) + g - 1) / g; }
+// The automatic choice takes the decode kernel for M <= 8 when its 16 waves cover K
+// (K <= 24576); longer reductions at decode sizes go to the prefill kernel, which takes
+// any K.
+static bool decode_fits(int M, int K) { return M <= kGemvMaxM && gemv_waves(K) <= 16; }
 
 // M = 1: the cross-wave reduction [waves-1][64][4] floats, then each wave's staged
 // activations [gpw * 64] halves. M > 1: each wave's staged rows, M * kStagedXRow bytes
@@ -606,7 +610,7 @@ int rlq_linear_native_kernel(int kernel, const void *x, int x_stride, int M, int
               "rlq_linear_native: unknown codebook %d", book);
   RLQ_REQUIRE(s_row && aligned(s_row, 4), "rlq_linear_native: null or misaligned row scales");
   RLQ_REQUIRE(kernel >= 0 && kernel <= 2, "rlq_linear_native_kernel: unknown kernel %d", kernel);
-  const bool gemv = kernel == 1 || (kernel == 0 && M <= kGemvMaxM);
+  const bool gemv = kernel == 1 || (kernel == 0 && decode_fits(M, K));
   auto st = static_cast<hipStream_t>(stream);
   auto xh = static_cast<const _Float16 *>(x);
   if (gemv) return run_gemv(book, xh, x_stride, M, K, N, packed, RLQ_F16, s_row, y, y_stride, accum, st);
@@ -634,7 +638,7 @@ int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int
   int rc = check_linear_args("rlq_linear_affine", x, x_stride, M, K, N, packed, scale_dtype, y, y_stride);
   if (rc) return rc;
   RLQ_REQUIRE(kernel >= 0 && kernel <= 2, "rlq_linear_affine_kernel: unknown kernel %d", kernel);
-  const bool gemv = kernel == 1 || (kernel == 0 && M <= kGemvMaxM);
+  const bool gemv = kernel == 1 || (kernel == 0 && decode_fits(M, K));
   auto st = static_cast<hipStream_t>(stream);
   auto xh = static_cast<const _Float16 *>(x);
   if (gemv) return run_gemv(kAffine, xh, x_stride, M, K, N, packed, scale_dtype, nullptr, y, y_stride, accum, st);

@@ -401,7 +401,22 @@ struct MoeArgs {
   const float *s_row;       // native books: row scales of the slots; slots[e]: expert e's slot
   const int *slots;
   int n_slots;
+  int n_experts;            // experts a work item may name (E + 1)
+  int n_rows;               // sorted rows of the call (T * S): the row -> token map and the outputs
 };
+
+// A work item as read from the list, clamped into the call's tables. The list is written
+// on the device; a corrupt entry then gives bounded wrong rows instead of an access outside
+// the weight stack, the row -> token map or the outputs.
+__device__ __forceinline__ int4 clamp_item(int4 it, int n_experts, int n_rows) {
+  it.x = min(max(it.x, 0), n_experts - 1);
+  it.y = min(max(it.y, 0), n_rows - 1);
+  it.z = min(max(it.z, 0), min(16, n_rows - it.y));
+  return it;
+}
+
+// The token of sorted row r, clamped to the call's tokens (see clamp_item).
+__device__ __forceinline__ int token_of(const int *tok, int r, int T) { return min(max(tok[r], 0), T - 1); }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
@@ -424,7 +439,7 @@ __device__ __forceinline__ void expert_tile(const MoeArgs &a, int e, int r0, int
 
   const bool live = c16 < rows;
   int xrow = r0 + (live ? c16 : 0);
-  if constexpr (KIND == 0) xrow = ONE_TOKEN ? 0 : a.tok[xrow];
+  if constexpr (KIND == 0) xrow = ONE_TOKEN ? 0 : token_of(a.tok, xrow, a.x_rows);
   const uint32_t xrange = wn > 0 ? (uint32_t)((a.x_rows - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
   f32x4 acc = tile_dot_rows<GPW, SD>(wt, rx, (uint32_t)xrow * a.x_stride * 2u + 16u * j4, live, wn, lane);
@@ -461,7 +476,8 @@ __global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
   const int n_items = *a.n_items;
   asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
   if (item >= n_items) return;                  // uniform: the whole workgroup leaves
-  expert_tile<GPW, SD, KIND, false>(a, it.x, it.y, it.z, lds);
+  const int4 ic = clamp_item(it, a.n_experts, a.n_rows);
+  expert_tile<GPW, SD, KIND, false>(a, ic.x, ic.y, ic.z, lds);
 }
 
 // One token: its routing and the gate/up products in one launch. Every workgroup picks the
@@ -536,8 +552,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
   const int n_items = *a.n_items;
   asm volatile("" ::"s"(it.x), "s"(it.y), "s"(it.z), "s"(n_items));   // both loads before the branch
   if (item >= n_items) return;                  // uniform: the whole workgroup leaves
-  int e = it.x;
-  const int r0 = it.y, rows = it.z;
+  const int4 ic = clamp_item(it, a.n_experts, a.n_rows);
+  int e = ic.x;
+  const int r0 = ic.y, rows = ic.z;
   bool slot_ok = true;
   if constexpr (BOOK != kAffine) {
     const int slot = __builtin_amdgcn_readfirstlane(a.slots[e]);
@@ -567,7 +584,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)((size_t)a.x_rows * a.x_stride * 2));
   auto load_row = [&](int row, u32x4 (&xr)[CPL]) {
     const bool ok = row < rows;
-    const int src = KIND == 0 ? a.tok[r0 + (ok ? row : 0)] : r0 + row;
+    const int src = KIND == 0 ? token_of(a.tok, r0 + (ok ? row : 0), a.x_rows) : r0 + row;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = lane + 64 * j;
@@ -681,7 +698,7 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(MoeArgs a, const
   // and, for the combining threads, the residual value the sum is added to.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool table = (int)threadIdx.x < A;
-  const int inv_r = table ? inv[threadIdx.x] : 0;
+  const int inv_r = table ? min(max(inv[threadIdx.x], 0), A - 1) : 0;
   const float w_r = table ? w[threadIdx.x] : 0.0f;
   float *hp = h + (size_t)t * h_stride + 16 * blockIdx.x + c;
   const float h_r = t < T ? *hp : 0.0f;
@@ -697,7 +714,7 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(MoeArgs a, const
   const uint32_t xrange = (uint32_t)((a.x_rows - 1) * a.x_stride + wn * kGroup) * 2u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, xrange);
   for (int item = wave; item < n_items; item += waves) {
-    const int4 it = item == wave ? it0 : a.items[item];
+    const int4 it = clamp_item(item == wave ? it0 : a.items[item], a.n_experts, A);
     int e = it.x;
     const int r0 = it.y, rows = it.z;
     bool ok = true;
@@ -888,6 +905,8 @@ static int gate_up_args(const void *x, int x_stride, int T, int H, int I, int E,
   a.K = H;
   a.tiles_per_expert = 2 * I / 16;
   a.out_stride = act_stride;
+  a.n_experts = E + 1;
+  a.n_rows = T * (topk + 1);
   return 0;
 }
 
@@ -1265,6 +1284,8 @@ int rlq_moe_down(const void *act, int act_stride, int T, int H, int I, int E, in
   a.K = I;
   a.tiles_per_expert = H / 16;
   a.out_stride = y_stride;
+  a.n_experts = E + 1;
+  a.n_rows = (int)A;
   return launch_expert<1>(I, scale_dtype, a.tiles_per_expert, moe_max_items(T, E, topk), T,
                           static_cast<hipStream_t>(stream), a);
 }
@@ -1334,6 +1355,8 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
   if (T <= kDownCombineTokens && expert_gpw(I) == 8 && I / kGroup <= 8) {
     // a few tokens: down and combine in one launch (the same bits as the two below)
     RLQ_REQUIRE(h && h_stride >= H, "rlq_moe: h is null or h_stride=%d < H=%d", h_stride, H);
+    RLQ_REQUIRE(packed_dn && aligned(packed_dn, 16), "rlq_moe: the down stack is null or not 16-byte aligned");
+    RLQ_REQUIRE(scale_dtype == RLQ_F16 || scale_dtype == RLQ_BF16, "rlq_moe: unknown scale dtype %d", scale_dtype);
     MoeArgs a = {};
     a.x = act;
     a.codes = static_cast<const u32x4 *>(packed_dn);
@@ -1344,6 +1367,8 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
     a.x_stride = I;
     a.K = I;
     a.tiles_per_expert = H / 16;
+    a.n_experts = E + 1;
+    a.n_rows = (int)A;
     const int waves = (int)std::min<size_t>(std::min<size_t>(16, A), moe_max_items(T, E, topk));
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (scale_dtype == RLQ_F16)
@@ -1406,6 +1431,8 @@ int rlq_moe_linear_native(const void *a, int a_stride, int a_rows, const int *to
     m.s_row = s;
     m.slots = slots;
     m.n_slots = n_slots;
+    m.n_experts = 1 << 30;                     // the slot table's size is the caller's; slots are checked
+    m.n_rows = a_rows;
     const int sub = staged_gpw(K) / expert_gpw(K);
     int rc;
     if (staged_gpw(K) == 8)
@@ -1506,6 +1533,9 @@ int rlq_moe_native(const void *x, int x_stride, const float *logits, int logit_s
               "rlq_moe_native: workspace of %zu bytes is smaller than the %zu this call needs", workspace_bytes, need);
   RLQ_REQUIRE(aligned(workspace, 256), "rlq_moe_native: workspace must be 256-byte aligned");
   RLQ_REQUIRE(h && h_stride >= H, "rlq_moe_native: h is null or h_stride=%d < H=%d", h_stride, H);
+  // the slot-stack bounds of the step-by-step entry points, ahead of the fused paths
+  RLQ_REQUIRE(n_slots >= 1 && (long long)n_slots * 2 * I <= (1LL << 30) && (long long)n_slots * H <= (1LL << 30),
+              "rlq_moe_native: %d slots of %d gate/up and %d down rows", n_slots, 2 * I, H);
   const size_t A = (size_t)T * (topk + 1);
   char *p = static_cast<char *>(workspace);
   int *sel = reinterpret_cast<int *>(p);            p += align256(A * 4);
@@ -1551,6 +1581,8 @@ int rlq_moe_native(const void *x, int x_stride, const float *logits, int logit_s
     a.x_stride = I;
     a.K = I;
     a.tiles_per_expert = H / 16;
+    a.n_experts = E + 1;
+    a.n_rows = (int)A;
     const int waves = (int)std::min<size_t>(std::min<size_t>(16, A), moe_max_items(T, E, topk));
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (book == RLQ_BOOK_INT15)

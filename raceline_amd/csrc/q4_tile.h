@@ -23,21 +23,22 @@
 // One group of 64 inputs is two MFMA steps s = 0, 1 (k = 64g + 32s .. +31); lane (c, j) =
 // (l%16, l/16) feeds uint32 word 8g + 4s + j of row c (k = 64g + 32s + 8j .. +7).
 //
-// Operand trick: a uint32 of eight codes becomes four fp16 pairs with five ops,
-//   d0 = u & 0x000F000F -> (q0, q4)          d1 = u & 0x00F000F0 -> (16 q1, 16 q5)
-//   d2 = (u>>8) & 0x000F000F -> (q2, q6)     d3 = (u>>8) & 0x00F000F0 -> (16 q3, 16 q7)
-// each half being the subnormal (code or 16 * code) * 2^-24, exact. The activation
-// operand carries the same element order with the odd elements divided by 16:
-//   (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16),
-// so one MFMA step sums x_e * q_e * 2^-24 over the eight elements. (x/16 is exact unless
-// |x| < 2^-10, where it rounds to the fp16 subnormal grid: an error below 2^-25 * 16 * 15
-// per such element.) The f16 MFMA of gfx950 sums products of subnormal operands with
-// about five bits less precision than normal ones (measured: 3.4e-6 of a group's rms
-// against 1e-7), so only the codes take this fast path: the group sums come from a second
-// MFMA against the normal constant (1, 1, 16, 16, ...), which undoes the 1/16 and lands
-// them in the accumulator layout. Per group, acc += (s * 2^24) * part + b * gsum in fp32
-// (both rescalings exact). An MFMA output row depends only on its own operand row, so a
-// token's result does not depend on which other tokens share the tile.
+// Operand trick: a uint32 of eight codes becomes four fp16 pairs with seven ops,
+//   d0 = u & 0x000F000F -> (q0, q4)          d1 = (u>>4) & 0x000F000F -> (q1, q5)
+//   d2 = (u>>8) & 0x000F000F -> (q2, q6)     d3 = (u>>12) & 0x000F000F -> (q3, q7)
+// each half being the subnormal code * 2^-24, exact. The activation operand carries the
+// same element order, (x0, x4, x1, x5, x2, x6, x3, x7): a permutation of the fp16 values
+// the caller passed, with nothing rounded, so one MFMA step sums x_e * q_e * 2^-24 over
+// the eight elements for activations of any magnitude. The f16 MFMA of gfx950 sums
+// products of subnormal operands with about five bits less precision than normal ones
+// (measured: 4e-6 of a group's rms against 1e-7, at every activation scale from 3e-5 to
+// 300; the loss is relative, not a floor), so only the codes take this fast path: the
+// group sums come from a second MFMA against a constant operand of ones, which lands them
+// in the accumulator layout. Per group, acc += (s * 2^24) * part + b * gsum in fp32 (both
+// rescalings exact). An MFMA output row depends only on its own operand row, so a token's
+// result does not depend on which other tokens share the tile.
+// (The prefill GEMM uses a cheaper five-op form of the codes, with the odd codes at 16 times
+// the scale, behind an exact per-row power-of-two prescale of the activations: gemm.hip.)
 #pragma once
 
 #include "rlq_common.h"
@@ -64,6 +65,19 @@ __host__ __device__ inline int gate_up_source_row(int n, int I) {
   return e * 2 * I + (c < 8 ? 8 * j + c : I + 8 * j + (c - 8));
 }
 
+// eight codes (element e at bits 4e) -> (q0, q4, q1, q5, q2, q6, q3, q7) * 2^-24, fp16 subnormals
+__device__ __forceinline__ half8 nib8_to_half8_sub(uint32_t u) {
+  u32x4 d;
+  d[0] = u & 0x000F000Fu;
+  d[1] = (u >> 4) & 0x000F000Fu;
+  d[2] = (u >> 8) & 0x000F000Fu;
+  d[3] = (u >> 12) & 0x000F000Fu;
+  return __builtin_bit_cast(half8, d);
+}
+
+// The five-op form for the prefill GEMM: (q0, q4, 16 q1, 16 q5, q2, q6, 16 q3, 16 q7) * 2^-24,
+// for activations in the matching order with the odd ones divided by 16 (gemm.hip prescales
+// each row by a power of two first, so that the division rounds nothing that matters).
 __device__ __forceinline__ half8 nib8_to_half8_oddx16(uint32_t u) {
   const uint32_t t = u >> 8;
   u32x4 d;
@@ -74,15 +88,14 @@ __device__ __forceinline__ half8 nib8_to_half8_oddx16(uint32_t u) {
   return __builtin_bit_cast(half8, d);
 }
 
-// eight consecutive activations -> operand order (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16)
+// eight consecutive activations -> operand order (x0, x4, x1, x5, x2, x6, x3, x7): a
+// permutation of the halves, exact
 __device__ __forceinline__ u32x4 prep_x8(u32x4 p) {
-  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-  const half2v sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
   u32x4 r;
   r[0] = __builtin_amdgcn_perm(p[2], p[0], 0x05040100u);  // (x0, x4)
-  r[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(p[2], p[0], 0x07060302u)) * sixteenth);
+  r[1] = __builtin_amdgcn_perm(p[2], p[0], 0x07060302u);  // (x1, x5)
   r[2] = __builtin_amdgcn_perm(p[3], p[1], 0x05040100u);  // (x2, x6)
-  r[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(p[3], p[1], 0x07060302u)) * sixteenth);
+  r[3] = __builtin_amdgcn_perm(p[3], p[1], 0x07060302u);  // (x3, x7)
   return r;
 }
 
@@ -158,12 +171,11 @@ __device__ __forceinline__ void native_step(f32x4 &acc, f32x4 &asum, const half8
 
 
 // The activation sums of one group for 16 token rows, as two products with a constant
-// operand (lane (c16, j4) gets rows 4 j4 + v; the 16 of the odd positions undoes the 1/16
-// that prep_x8 puts on the odd codes' activations). Every tile of the same rows needs the
-// same sums: a caller that forms them once and hands them to group_step_gs gets the bits
-// group_step gets.
+// operand of ones (lane (c16, j4) gets rows 4 j4 + v). Every tile of the same rows needs
+// the same sums: a caller that forms them once and hands them to group_step_gs gets the
+// bits group_step gets.
 __device__ __forceinline__ f32x4 group_sums(const half8 (&af)[2]) {
-  const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x4C004C00u, 0x3C003C00u, 0x4C004C00u});  // 1, 16
+  const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
   f32x4 gsv = {};
 #pragma unroll
   for (int s = 0; s < 2; ++s) gsv = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, gsv, 0, 0, 0);
@@ -178,7 +190,7 @@ __device__ __forceinline__ void group_step_gs(f32x4 &acc, const half8 (&af)[2], 
   f32x4 p = {};
 #pragma unroll
   for (int s = 0; s < 2; ++s)
-    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], nib8_to_half8_oddx16(wq[jg >> 1][2 * (jg & 1) + s]), p, 0, 0, 0);
+    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], nib8_to_half8_sub(wq[jg >> 1][2 * (jg & 1) + s]), p, 0, 0, 0);
   const uint32_t pr = sq[jg >> 2][jg & 3];
   const float sc = fma_scale<SD, 0>(pr, kTwo24, 0.0f);   // s * 2^24, exact: undoes the codes' 2^-24
 #pragma unroll

@@ -217,6 +217,19 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
             int H, int I, const void *packed_gu, const void *packed_dn, int scale_dtype, float *h, int h_stride,
             void *workspace, size_t workspace_bytes, void *stream);
 
+/* rlq_moe without a workspace argument. It has no counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops
+ * and harnesses that forbid hipMalloc). Its scratch is a static device array of
+ * rlq_moe_no_alloc_max_bytes() bytes (48 MiB: the BASELINE MoE layer up to 512 tokens) that
+ * each GPU holds from the library's first use there until the process ends; a call whose
+ * rlq_moe_workspace_bytes exceeds it fails with an error. The call allocates nothing. Every
+ * call on one GPU shares that array, so calls that overlap on one GPU (two streams or two
+ * threads) race; calls in order on one stream do not. Same results as rlq_moe. */
+size_t rlq_moe_no_alloc_max_bytes(void);
+int rlq_moe_no_alloc(const void *x, int x_stride, const float *logits, int logit_stride, int T, int E, int topk,
+                     int norm_topk, int H, int I, const void *packed_gu, const void *packed_dn, int scale_dtype,
+                     float *h, int h_stride, void *stream);
+
 /* ---------------------------------------------------------------- native experts */
 
 /* The experts of one kind (gate_up or down) in the native format, one launch: replaces

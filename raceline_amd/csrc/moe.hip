@@ -29,6 +29,7 @@
 #include "../../include/rlq.h"
 
 #include <algorithm>
+#include <mutex>
 #include <cmath>
 
 namespace rlq {
@@ -1384,6 +1385,64 @@ int rlq_moe(const void *x, int x_stride, const float *logits, int logit_stride, 
   return rlq_moe_combine(y, H, inv, w, T, topk, H, h, h_stride, stream);
 }
 
+
+}  // extern "C"
+
+namespace rlq {
+
+// The scratch of rlq_moe_no_alloc: the workspace of one MoE layer call (routing tables,
+// SwiGLU activations, expert outputs) in a file-scope device array. Each GPU the library
+// runs on holds its own copy from the first use there until the process ends. 48 MiB
+// holds the BASELINE MoE layer up to 512 tokens (rlq_moe_workspace_bytes(512, 256, 8,
+// 2048, 512) is 42.5 MB) and any decode batch.
+constexpr size_t kMoeScratchBytes = (size_t)48 << 20;
+__device__ __align__(256) unsigned char scratch[kMoeScratchBytes];
+
+// The array's device address on the current device, looked up once per device. In host
+// code `scratch` names a host-side stand-in, not device memory: only this address may be
+// handed to kernels.
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxScratchDevices];
+
+static int scratch_address(void **out) {
+  int dev = -1;
+  RLQ_HIP(hipGetDevice(&dev));
+  RLQ_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "rlq_moe_no_alloc: device %d is past the %d it supports", dev,
+              kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    RLQ_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    RLQ_REQUIRE(p != nullptr && aligned(p, 256), "rlq_moe_no_alloc: no usable scratch address on device %d", dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace rlq
+
+extern "C" {
+
+size_t rlq_moe_no_alloc_max_bytes(void) { return rlq::kMoeScratchBytes; }
+
+int rlq_moe_no_alloc(const void *x, int x_stride, const float *logits, int logit_stride, int T, int E, int topk,
+                     int norm_topk, int H, int I, const void *packed_gu, const void *packed_dn, int scale_dtype,
+                     float *h, int h_stride, void *stream) {
+  using namespace rlq;
+  if (int rc = check_moe_shape("rlq_moe_no_alloc", T, E, topk, H, I)) return rc;
+  const size_t need = rlq_moe_workspace_bytes(T, E, topk, H, I);
+  RLQ_REQUIRE(need <= kMoeScratchBytes,
+              "rlq_moe_no_alloc: T=%d E=%d topk=%d H=%d I=%d needs %zu bytes of scratch, more than the %zu it holds "
+              "(use rlq_moe with a workspace)", T, E, topk, H, I, need, kMoeScratchBytes);
+  void *ws = nullptr;
+  if (int rc = scratch_address(&ws)) return rc;
+  // rlq_moe needs no initialised workspace: every table and intermediate it reads is
+  // written earlier in the same call
+  return rlq_moe(x, x_stride, logits, logit_stride, T, E, topk, norm_topk, H, I, packed_gu, packed_dn, scale_dtype, h,
+                 h_stride, ws, kMoeScratchBytes, stream);
+}
 
 int rlq_moe_linear_native(const void *a, int a_stride, int a_rows, const int *tok, int K, int Ne, const void *packed,
                           const float *s, const int *slots, int n_slots, int book, const int *items, const int *n_items,

@@ -68,6 +68,9 @@ SIGNATURES = {
                                        c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p]),
     "rlq_moe": (c_int, [c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p,
                         c_void_p, c_int, c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    "rlq_moe_no_alloc_max_bytes": (c_size_t, []),
+    "rlq_moe_no_alloc": (c_int, [c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                 c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p]),
 }
 
 

@@ -91,3 +91,15 @@ def test_errors_are_fatal_by_default():
     assert r.returncode == 1
     assert "raceline: fatal: rlq_linear_affine: K=100 is not a multiple of the group size 64" in r.stderr
     assert "not reached" not in r.stdout
+
+
+def test_no_alloc_moe_refuses_sizes_past_its_scratch():
+    """rlq_moe_no_alloc holds a fixed scratch array; a call that needs more is refused with an
+    error naming the limit, before any device work."""
+    L = lib.load()
+    cap = L.rlq_moe_no_alloc_max_bytes()
+    assert cap == 48 << 20
+    assert L.rlq_moe_workspace_bytes(512, 256, 8, 2048, 512) <= cap
+    assert L.rlq_moe_workspace_bytes(4096, 256, 8, 2048, 512) > cap
+    with pytest.raises(lib.RlqError, match="more than the 50331648 it holds"):
+        lib.call("rlq_moe_no_alloc", 16, 2048, 16, 257, 4096, 256, 8, 1, 2048, 512, 16, 16, 0, 16, 2048, None)

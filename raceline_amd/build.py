@@ -38,11 +38,13 @@ def hipcc() -> str:
 
 
 def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    """HIP sources (kernels and their entry points) and host-only C++ (the model file reader)."""
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
 def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
+    base = os.path.basename(src)
+    obj = os.path.join(BUILD, base.rsplit(".", 1)[0] + (".o" if base.endswith(".hip") else ".cpp.o"))
     cmd = [hipcc(), *HIP_FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:

@@ -25,7 +25,9 @@ struct GemmArgs {
 // sums; kInt16: group and row sums; a shape whose K is split: the second half's partials).
 size_t gemm4_workspace(int book, int M, int K, int N);
 
-int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
+// codes, sbq: the two sections of a packed matrix (q4_tile.h), or of rows [r0, r0 + N) of a
+// larger one (r0 a multiple of 16: see packed_tile_offsets in linear.h).
+int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes, const void *sbq, int sd,
               const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st);
 
 // defined in linear.hip

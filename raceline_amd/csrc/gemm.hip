@@ -502,7 +502,7 @@ static int launch_gemm4_inst(int accum, dim3 grid, size_t lds, hipStream_t st, c
   return 0;
 }
 
-int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
+int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes, const void *sbq, int sd,
               const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st) {
   const int G = K / kGroup;
   const size_t need = gemm4_workspace(book, M, K, N);
@@ -510,8 +510,8 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
   RLQ_REQUIRE(need == 0 || aligned(ws, 256), "workspace must be 256-byte aligned");
   RLQ_REQUIRE((size_t)M * std::max(x_stride, K) * 2 < (1ull << 31), "prefill kernel: x spans more than 2 GiB");
   GemmArgs a = {};
-  a.codes = static_cast<const u32x4 *>(packed);
-  a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
+  a.codes = static_cast<const u32x4 *>(codes);
+  a.sb = static_cast<const u32x4 *>(sbq);
   a.srow = srow;
   a.y = y;
   a.M = M; a.K = K; a.N = N; a.y_stride = y_stride;

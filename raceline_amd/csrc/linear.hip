@@ -12,6 +12,7 @@
 // The packed layout, the MFMA operand layout and the operand trick are described in
 // q4_tile.h.
 #include "gemm.h"
+#include "linear.h"
 #include "q4_tile.h"
 #include "../../include/rlq.h"
 
@@ -426,16 +427,16 @@ static int launch_gemv(int book, int sd, int accum, dim3 grid, int threads, size
 
 // book: kAffine (packed holds codes then scale/bias quads; sd their dtype) or a native
 // codebook (packed holds codes only; srow the row scales).
-static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *packed, int sd,
-                    const float *srow, float *y, int y_stride, int accum, hipStream_t st) {
+static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes, const void *sbq,
+                    int sd, const float *srow, float *y, int y_stride, int accum, hipStream_t st) {
   RLQ_REQUIRE(M <= kGemvMaxM, "decode kernel handles M <= %d rows (got %d)", kGemvMaxM, M);
   const int gpw = gemv_gpw(K), waves = gemv_waves(K);
   RLQ_REQUIRE(waves <= 16, "decode kernel: K=%d is larger than the %d it supports", K, 16 * 24 * kGroup);
   const size_t lds = gemv_lds_bytes(M, waves, gpw);
   GemvArgs a;
   a.x = x;
-  a.codes = static_cast<const u32x4 *>(packed);
-  a.sb = reinterpret_cast<const u32x4 *>(static_cast<const char *>(packed) + packed_code_bytes(K, N));
+  a.codes = static_cast<const u32x4 *>(codes);
+  a.sb = static_cast<const u32x4 *>(sbq);
   a.srow = srow;
   a.y = y;
   a.x_stride = x_stride; a.M = M; a.K = K; a.N = N; a.y_stride = y_stride;
@@ -454,6 +455,15 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
   if (rc) return rc;
   RLQ_HIP(hipGetLastError());
   return 0;
+}
+
+int linear_packed(int kernel, int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes,
+                  const void *sbq, int sd, const float *srow, float *y, int y_stride, int accum, void *ws,
+                  size_t ws_bytes, hipStream_t st) {
+  RLQ_REQUIRE(kernel >= 0 && kernel <= 2, "unknown kernel %d", kernel);
+  const bool gemv = kernel == 1 || (kernel == 0 && decode_fits(M, K));
+  if (gemv) return run_gemv(book, x, x_stride, M, K, N, codes, sbq, sd, srow, y, y_stride, accum, st);
+  return run_gemm4(book, x, x_stride, M, K, N, codes, sbq, sd, srow, y, y_stride, accum, ws, ws_bytes, st);
 }
 
 // ================================================================== group sums
@@ -610,12 +620,9 @@ int rlq_linear_native_kernel(int kernel, const void *x, int x_stride, int M, int
               "rlq_linear_native: unknown codebook %d", book);
   RLQ_REQUIRE(s_row && aligned(s_row, 4), "rlq_linear_native: null or misaligned row scales");
   RLQ_REQUIRE(kernel >= 0 && kernel <= 2, "rlq_linear_native_kernel: unknown kernel %d", kernel);
-  const bool gemv = kernel == 1 || (kernel == 0 && decode_fits(M, K));
-  auto st = static_cast<hipStream_t>(stream);
-  auto xh = static_cast<const _Float16 *>(x);
-  if (gemv) return run_gemv(book, xh, x_stride, M, K, N, packed, RLQ_F16, s_row, y, y_stride, accum, st);
-  return run_gemm4(book, xh, x_stride, M, K, N, packed, RLQ_F16, s_row, y, y_stride, accum, workspace, workspace_bytes,
-                   st);
+  // native matrices have no scale/bias section: the codes stand in for it (never read)
+  return linear_packed(kernel, book, static_cast<const _Float16 *>(x), x_stride, M, K, N, packed, packed, RLQ_F16,
+                       s_row, y, y_stride, accum, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int rlq_linear_native(const void *x, int x_stride, int M, int K, int N, const void *packed, const float *s_row,
@@ -638,12 +645,9 @@ int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int
   int rc = check_linear_args("rlq_linear_affine", x, x_stride, M, K, N, packed, scale_dtype, y, y_stride);
   if (rc) return rc;
   RLQ_REQUIRE(kernel >= 0 && kernel <= 2, "rlq_linear_affine_kernel: unknown kernel %d", kernel);
-  const bool gemv = kernel == 1 || (kernel == 0 && decode_fits(M, K));
-  auto st = static_cast<hipStream_t>(stream);
-  auto xh = static_cast<const _Float16 *>(x);
-  if (gemv) return run_gemv(kAffine, xh, x_stride, M, K, N, packed, scale_dtype, nullptr, y, y_stride, accum, st);
-  return run_gemm4(kAffine, xh, x_stride, M, K, N, packed, scale_dtype, nullptr, y, y_stride, accum, workspace,
-                   workspace_bytes, st);
+  const void *sbq = static_cast<const char *>(packed) + packed_code_bytes(K, N);
+  return linear_packed(kernel, kAffine, static_cast<const _Float16 *>(x), x_stride, M, K, N, packed, sbq, scale_dtype,
+                       nullptr, y, y_stride, accum, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int rlq_linear_affine(const void *x, int x_stride, int M, int K, int N, const void *packed, int scale_dtype, float *y,

@@ -68,6 +68,31 @@ SIGNATURES = {
                                        c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p]),
     "rlq_moe": (c_int, [c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p,
                         c_void_p, c_int, c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    # include/rl_engine.h: the model file reader and the engine layer
+    "rlm_open": (c_void_p, [c_char_p]),
+    "rlm_close": (None, [c_void_p]),
+    "rlm_config_int": (c_int, [c_void_p, c_char_p]),
+    "rlm_tensor": (c_int, [c_void_p, c_char_p, c_void_p]),
+    "rlm_tensor_part": (c_int, [c_void_p, c_char_p, c_char_p, c_void_p, c_void_p]),
+    "rlm_section": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "rl_open": (c_void_p, [c_char_p, c_int, c_int]),
+    "rl_close": (None, [c_void_p]),
+    "rl_vocab": (c_int, [c_void_p]),
+    "rl_hidden_size": (c_int, [c_void_p]),
+    "rl_linear": (c_int, [c_void_p, c_char_p, c_char_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int, c_void_p]),
+    "rl_norm": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p]),
+    "rl_mlp": (c_int, [c_void_p, c_int, c_void_p, c_int, c_int, c_void_p]),
+    "rl_head": (c_void_p, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "rl_set_draft_vocab": (None, [c_void_p, c_int]),
+    "rl_set_draft_tail": (None, [c_void_p, c_int]),
+    "rl_draft_main": (c_int, [c_void_p]),
+    "rl_draft_tail": (c_int, [c_void_p]),
+    "rl_draft_vocab": (c_int, [c_void_p]),
+    "rl_logits_stride": (c_size_t, [c_void_p]),
+    "rl_draft_head": (c_void_p, [c_void_p, c_void_p, c_void_p]),
+    "rl_top_k": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "rl_top_k_device": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "rl_argmax": (c_int, [c_void_p]),
     "rlq_moe_no_alloc_max_bytes": (c_size_t, []),
     "rlq_moe_no_alloc": (c_int, [c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                  c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p]),

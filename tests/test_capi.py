@@ -21,7 +21,7 @@ def declared_functions():
         text = open(path).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         text = re.sub(r"//[^\n]*", "", text)
-        names += re.findall(r"\b(rlq_\w+)\s*\(", text)
+        names += re.findall(r"\b((?:rlq|rlm|rl)_\w+)\s*\(", text)
     return sorted(set(names))
 
 
@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
     assert set(declared_functions()) <= set(lib.SIGNATURES)
     nm = subprocess.run(["nm", "-D", "--defined-only", lib.library_path()], capture_output=True, text=True)
     if nm.returncode == 0:
-        exported = set(re.findall(r"\b(rlq_\w+)\b", nm.stdout))
+        exported = set(re.findall(r"\b((?:rlq|rlm|rl)_\w+)\b", nm.stdout))
         assert set(declared_functions()) <= exported
 
 

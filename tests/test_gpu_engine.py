@@ -1,0 +1,229 @@
+"""The engine layer on the GPU (include/rl_engine.h) over .rlm files written with the product
+writer, against the oracle:
+
+- rl_linear on every tensor kind (q4a with bf16 scales, q4n int15 and fp4, f16b) and on the
+  parts of stacked tensors, with and without ACCUM (Engine::encode_linear,
+  src/engine.mm:832-906): max|err|/rms <= 1e-3 of the fp64 product.
+- rl_norm (rms_norm_rows, kernels/ops.metal:74-112, with the native column-scale fold of
+  engine.mm:517-530): each half within one fp16 ulp of the fp64 value rounded once.
+- rl_mlp, dense (encode_mlp, engine.mm:943-958) and mixture of experts (encode_moe,
+  :965-1059; native and affine stacks): the MLP's contribution within 1e-3; a token's
+  result is the same bits whatever other tokens share the call, within one kernel family
+  (the decode kernel up to 8 rows, the prefill kernel above; the MoE kernels throughout).
+- rl_head and the draft head (engine.mm:1425-1458,1634-1638): logits within 1e-3; the draft
+  logits are exactly the main and tail slices of the full head's; rl_top_k_device and
+  rl_argmax give rl_top_k's ids and values exactly.
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import oracle.engine as OE
+from raceline_amd.model import Engine, top_k
+from tests import model_files as MF
+from tests.qdata import to_dev
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+BOOKS = [None, "int15", "fp4"]
+
+
+def _sync():
+    import torch
+
+    torch.cuda.synchronize()
+
+
+def _x(seed, rows, k, scale=1.0):
+    return (np.random.default_rng(seed).standard_normal((rows, k)) * scale).astype(np.float16)
+
+
+def _col_scale(m, name):
+    return m.native[name][2] if name in m.native else None
+
+
+@pytest.mark.parametrize("book", BOOKS)
+def test_linear_every_kind_and_part(gpu, tmp_path, book):
+    m = MF.write_dense_model(str(tmp_path / "m.rlm"), seed=10, native_book=book)
+    with Engine(m.path, max_chunk=64) as e:
+        assert e.vocab == 1000 and e.hidden_size == 256 and e.logits_stride == 1024
+        for rows in (1, 5, 40):                               # decode kernel, and prefill at 40
+            x = _x(rows, rows, 256)
+            xd = to_dev(x, gpu)
+            for name, part, r in (("layers.0.attn.qkv", None, (0, 1024)), ("layers.0.attn.qkv", "k", (512, 768)),
+                                  ("layers.1.attn.qkv", "v", (768, 1024)), ("layers.1.mlp.gate_up", "up", (512, 1024)),
+                                  ("lm_head", None, (0, 1000)), ("extra.dense", None, (0, 300))):
+                y = e.linear(name, xd, part=part, n=r[1] - r[0])
+                _sync()
+                ref = MF.linear_f64(m, name, x, rows=r)
+                O.check_close(y.cpu().numpy(), ref, TOL, f"{name}[{part}] rows={rows} book={book}")
+            act = _x(rows + 50, rows, 512, 0.1)
+            h0 = np.random.default_rng(rows).standard_normal((rows, 256)).astype(np.float32)
+            h = to_dev(h0, gpu)
+            e.linear("layers.1.mlp.down", to_dev(act, gpu), out=h, accum=True)
+            _sync()
+            ref = h0 + MF.linear_f64(m, "layers.1.mlp.down", act)
+            O.check_close(h.cpu().numpy(), ref, TOL, f"down accum rows={rows} book={book}")
+
+
+def _check_half(got, ref, what):
+    ref = np.asarray(ref, np.float64)
+    bound = 2.0 ** -10 * np.abs(ref) + 2.0 ** -24
+    bad = np.abs(np.asarray(got, np.float64) - ref) > bound
+    assert not bad.any(), f"{what}: {bad.sum()} halves off by more than one ulp"
+
+
+@pytest.mark.parametrize("book", BOOKS)
+def test_norm(gpu, tmp_path, book):
+    m = MF.write_dense_model(str(tmp_path / "m.rlm"), seed=11, native_book=book)
+    eps = m.cfg["rms_norm_eps"]
+    h0 = (np.random.default_rng(12).standard_normal((9, 256)) * 3.0).astype(np.float32)
+    with Engine(m.path, max_chunk=16) as e:
+        for which, layer, fname, consumer in ((0, 1, "layers.1.in_norm", "layers.1.attn.qkv"),
+                                              (1, 0, "layers.0.post_norm", "layers.0.mlp.gate_up"),
+                                              (2, 0, "final_norm", "lm_head")):
+            xn = e.norm(which, layer, to_dev(h0, gpu))
+            _sync()
+            w = m.floats[fname].astype(np.float64)
+            c = _col_scale(m, consumer)
+            if c is not None:
+                w = (m.floats[fname] * c[:256]).astype(np.float32).astype(np.float64)   # folded in fp32, as the engine does
+            ref = np.asarray(h0, np.float64) / np.sqrt(np.mean(np.asarray(h0, np.float64) ** 2, 1, keepdims=True) + eps) * w
+            _check_half(xn.cpu().numpy(), ref, f"norm {which} book={book}")
+            one = e.norm(which, layer, to_dev(h0[4:5].copy(), gpu))
+            _sync()
+            np.testing.assert_array_equal(one.cpu().numpy()[0], xn.cpu().numpy()[4])
+
+
+def _mlp_ref(m, layer, h0):
+    I = m.cfg["intermediate_size"]
+    gu, dn = f"layers.{layer}.mlp.gate_up", f"layers.{layer}.mlp.down"
+    w = m.floats[f"layers.{layer}.post_norm"]
+    cg = _col_scale(m, gu)
+    if cg is not None:
+        w = (w * cg).astype(np.float32)
+    return OE.mlp_dense_f64(h0, w, m.cfg["rms_norm_eps"], lambda xn: MF.linear_f64(m, gu, xn),
+                            lambda a: MF.linear_f64(m, dn, a), I, cs=_col_scale(m, dn))
+
+
+@pytest.mark.parametrize("book", BOOKS)
+def test_dense_mlp(gpu, tmp_path, book):
+    import torch
+
+    m = MF.write_dense_model(str(tmp_path / "m.rlm"), seed=13, native_book=book)
+    with Engine(m.path, max_chunk=64) as e:
+        for T in (1, 6, 40):
+            h0 = np.random.default_rng(T).standard_normal((T, 256)).astype(np.float32)
+            h = to_dev(h0, gpu)
+            e.mlp(1, h)
+            _sync()
+            ref = _mlp_ref(m, 1, h0)
+            O.check_close(h.cpu().numpy().astype(np.float64) - h0, ref - h0, TOL, f"dense MLP T={T} book={book}")
+            # a token's result does not depend on the other tokens of the call, within one kernel
+            # family: up to 8 rows (decode kernel) one row alone; above 8 (prefill kernel) a sub-batch
+            if T > 1:
+                lo = 0 if T <= 8 else T - 12
+                sub = to_dev(h0[lo:T].copy() if T > 8 else h0[T - 1:T].copy(), gpu)
+                e.mlp(1, sub)
+                _sync()
+                assert torch.equal(sub, h[lo:T] if T > 8 else h[T - 1:T])
+
+
+def _moe_ref(m, layer, h0):
+    cfg = m.cfg
+    E, topk, I, H = cfg["num_experts"], cfg["num_experts_per_tok"], cfg["moe_intermediate_size"], cfg["hidden_size"]
+    gu, dn = f"layers.{layer}.moe.gate_up", f"layers.{layer}.moe.down"
+    w = m.floats[f"layers.{layer}.post_norm"]
+    cg = _col_scale(m, gu)
+    if cg is not None:
+        w = (w * cg).astype(np.float32)
+    xn = OE.rms_norm_f16(h0, w, cfg["rms_norm_eps"])
+    logits = (xn.astype(np.float64) @ m.dense[f"layers.{layer}.moe.router"].astype(np.float64).T).astype(np.float32)
+    srt = np.sort(logits[:, :E], axis=1)[:, ::-1]
+    assert (srt[:, topk - 1] - srt[:, topk] > 1e-4).all(), "routing margin too small for a stable comparison"
+    if m.book:
+        (qg, sg, _, _), (qd, sd, cd, _) = m.native[gu], m.native[dn]
+        ref, _, _ = O.moe_layer_native_f64(xn, logits, (qg, sg), (qd, sd), cd, np.arange(E + 1), E, topk, I, H, m.book,
+                                           h0=h0)
+    else:
+        ref, _, _ = O.moe_layer_f64(xn, logits, m.affine[gu][:3], m.affine[dn][:3], E, topk, I, H, scale_dtype="bf16",
+                                    h0=h0)
+    return ref
+
+
+@pytest.mark.parametrize("book", BOOKS)
+def test_moe_mlp(gpu, tmp_path, book):
+    import torch
+
+    m = MF.write_moe_model(str(tmp_path / "moe.rlm"), seed=14, native_book=book)
+    with Engine(m.path, max_chunk=64) as e:
+        for T in (1, 3, 24):
+            h0 = np.random.default_rng(100 + T).standard_normal((T, 256)).astype(np.float32)
+            h = to_dev(h0, gpu)
+            e.mlp(0, h)
+            _sync()
+            ref = _moe_ref(m, 0, h0)
+            O.check_close(h.cpu().numpy().astype(np.float64) - h0, ref - h0, TOL, f"MoE T={T} book={book}")
+            if T > 1:
+                one = to_dev(h0[1:2].copy(), gpu)
+                e.mlp(0, one)
+                _sync()
+                assert torch.equal(one[0], h[1])
+
+
+@pytest.mark.parametrize("book", BOOKS)
+def test_head_draft_vocab_and_top_k(gpu, tmp_path, book):
+    import torch
+
+    m = MF.write_dense_model(str(tmp_path / "m.rlm"), seed=15, native_book=book)
+    h0 = np.random.default_rng(16).standard_normal((4, 256)).astype(np.float32)
+    with Engine(m.path, max_chunk=16) as e:
+        logits = e.head(to_dev(h0, gpu))
+        _sync()
+        w = m.floats["final_norm"]
+        c = _col_scale(m, "lm_head")
+        if c is not None:
+            w = (w * c).astype(np.float32)
+        xn = OE.rms_norm_f16(h0, w, m.cfg["rms_norm_eps"])
+        ref = MF.linear_f64(m, "lm_head", xn)
+        got = logits.cpu().numpy()
+        O.check_close(got[:, :1000], ref, TOL, f"head book={book}")
+        assert (got[:, 1000:] == 0).all()                     # padding rows of the head
+        # top-k of the vocabulary on the device, and rl_argmax, against rl_top_k
+        for k in (1, 8, 256):
+            ids, vals = e.top_k_device(logits[0, :1000].contiguous(), k)
+            rid, rvals = top_k(got[0, :1000], k)
+            assert ids == list(rid) and np.array_equal(np.float32(vals), rvals)
+        assert e.argmax() == int(np.argmax(got[0, :1000]))
+        # the draft vocabulary: the main rows, then the tail rows (native heads only)
+        e.set_draft_vocab(300)
+        e.set_draft_tail(800)
+        assert e.draft_main == 512
+        assert e.draft_tail == (768 if book else -1)
+        d = e.draft_head(to_dev(h0[2].copy(), gpu))
+        _sync()
+        full = e.head(to_dev(h0[2:3].copy(), gpu))[0]
+        _sync()
+        want = torch.cat([full[:512], full[768:]]) if book else full[:512]
+        assert e.draft_vocab == want.numel()
+        assert torch.equal(d, want)
+        e.set_draft_vocab(0)
+        e.set_draft_tail(-1)
+        assert e.draft_main == 1024 and e.draft_tail == -1 and e.draft_vocab == 1024
+
+
+def test_device_top_k_ties_nan_and_infinities(gpu, tmp_path):
+    m = MF.write_dense_model(str(tmp_path / "m.rlm"), seed=17, layers=1)
+    rng = np.random.default_rng(18)
+    with Engine(m.path, max_chunk=16) as e:
+        for n in (5, 3000, 16000):
+            x = rng.integers(-30, 30, n).astype(np.float32)
+            x[rng.random(n) < 0.1] = np.nan
+            x[rng.random(n) < 0.02] = -np.inf
+            x[rng.random(n) < 0.01] = np.inf
+            for k in (1, 7, 64, 256):
+                ids, vals = e.top_k_device(to_dev(x, gpu), k)
+                rid, rvals = top_k(x, k)
+                assert ids == list(rid), f"n={n} k={k}"
+                np.testing.assert_array_equal(np.float32(vals), rvals)

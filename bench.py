@@ -268,6 +268,43 @@ def bench_moe_native(device, steps, warmup):
     return out
 
 
+def bench_native_epilogue(device, steps, warmup):
+    """What the native linear's epilogue (the row scale) costs: linear_q4n against
+    linear_q4n_raw (kernels/linear.metal:226-252), native int15 codes, on the 9B gate_up
+    shape at M = 1 (over >= 1 GiB of copies) and the 27B gate_up at M = 2048."""
+    import torch
+
+    from raceline_amd import ops, synth
+
+    out = {}
+    for M, K, N in ((1, 4096, 24576), (2048, 5120, 34816)):
+        per = K * N // 2 + 4 * N
+        copies = max(2, -(-CACHE_DEFEAT_BYTES // per)) if M == 1 else 2
+        g = torch.Generator(device=device)
+        nws = []
+        for c in range(copies):
+            g.manual_seed(900 + c)
+            w = torch.randint(-(1 << 31), (1 << 31) - 1, (N, K // 8), generator=g, device=device, dtype=torch.int32)
+            nws.append(ops.pack_native(w, torch.rand(N, generator=g, device=device) * 0.01 + 0.001, "int15"))
+            del w
+        x = synth.random_activations(M, K, 901, device)
+        y = torch.empty((M, N), dtype=torch.float32, device=device)
+        ops._WS.get(device, ops.workspace_bytes(M, K, N))
+        res = {}
+        for name, fn in (("scaled", ops.linear_native), ("raw", ops.linear_native_raw)):
+            sg = StepGraphs([(lambda nw=nw, fn=fn: fn(x, nw, out=y)) for nw in nws])
+            t = time_steps(sg, steps if M == 1 else max(4, steps // 5), warmup if M == 1 else 2)
+            res[name] = t
+            del sg
+        key = f"native_int15_k{K}_n{N}_m{M}"
+        out[key] = {"scaled_us": round(res["scaled"] * 1e6, 2), "raw_us": round(res["raw"] * 1e6, 2),
+                    "epilogue_share": round(1 - res["raw"] / res["scaled"], 4)}
+        log(f"[bench] native linear {key}: {res['scaled'] * 1e6:.1f} us, raw {res['raw'] * 1e6:.1f} us")
+        del nws
+        torch.cuda.empty_cache()
+    return {"native_epilogue": out}
+
+
 def bench_prefill(device, steps, warmup):
     """the 27B layer's four projections at M = 2048 (fp16 activations with
     1% outliers x20), TFLOP/s against the dense fp16 MFMA peak; two weight copies."""
@@ -348,7 +385,7 @@ def bench_part(part, steps, warmup):
     lib.load()
     dev = torch.device("cuda:0")
     log(f"[bench] part {part}")
-    fn = {"prefill": bench_prefill, "moe": bench_moe, "decode": bench_decode}[part]
+    fn = {"prefill": bench_prefill, "moe": bench_moe, "decode": bench_decode, "epilogue": bench_native_epilogue}[part]
     return fn(dev, steps, warmup)
 
 
@@ -385,53 +422,147 @@ def time_kernel(layers, shapes, M, idx, device, launches, kernel=0, outliers=0.0
     return start.elapsed_time(end) / 1e3 / launches
 
 
-def cpu_baseline(device, budget_s=15.0):
-    """The reference's CPU path (numpy dequant + fp32 BLAS matmul, as restated in the
-    oracle) on the 9B layer at M=1 (q/k/v stacked, as the headline), weights copied from
-    the GPU inputs' generator."""
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu reports), from /proc/cpuinfo."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        return int(max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1]))
+    except Exception:  # noqa: BLE001
+        return int(os.environ.get("OPENBLAS_NUM_THREADS", os.cpu_count() or 1))
+
+
+def _median(v):
+    v = sorted(v)
+    return v[len(v) // 2]
+
+
+def _host_affine(device, K, N, seed):
     import numpy as np
     import torch
 
-    import oracle as O
     from raceline_amd import synth
-    from raceline_amd.configs import CFG2_9B_STACKED as L9, linear_bytes
 
-    try:
-        from threadpoolctl import threadpool_info
-        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:  # noqa: BLE001
-        blas_threads = int(os.environ.get("OPENBLAS_NUM_THREADS", os.cpu_count() or 1))
-    mats = []
-    for i, (_, K, N) in enumerate(L9):
-        w, s, b = synth.random_affine(N, K, 4242 + i, device, packed=False)
-        mats.append((K, N, w.cpu().numpy().view(np.uint32), s.cpu().view(torch.int16).numpy().view(np.uint16),
-                     b.cpu().view(torch.int16).numpy().view(np.uint16)))
-    x = {K: synth.random_activations(1, K, 5, device).cpu().numpy() for _, K, _ in L9}
-    total_bytes = 0
-    t_deq = t_mm = 0.0
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        for K, N, w, s, b in mats:
+    w, s, b = synth.random_affine(N, K, seed, device, packed=False)
+    return (w.cpu().numpy().view(np.uint32), s.cpu().view(torch.int16).numpy().view(np.uint16),
+            b.cpu().view(torch.int16).numpy().view(np.uint16))
+
+
+def _cpu_linear(mats, xs, runs):
+    """The reference's CPU path over a list of matrices (numpy unpack + dequant, then the
+    fp32 BLAS matmul): one warm-up, then the median of `runs` of each phase, in ms."""
+    import numpy as np
+
+    import oracle as O
+
+    deq, mm = [], []
+    for r in range(runs + 1):
+        td = tm = 0.0
+        for (w, s, b), x in zip(mats, xs):
             a = time.perf_counter()
-            q = O.unpack_nibbles_u32(w)
-            W = O.dequant_affine(q, s, b, "f16")
+            W = O.dequant_affine(O.unpack_nibbles_u32(w), s, b, "f16")
             m = time.perf_counter()
-            _ = x[K].astype(np.float32) @ W.T
+            _ = x.astype(np.float32) @ W.T
             e = time.perf_counter()
-            t_deq += m - a
-            t_mm += e - m
-            total_bytes += linear_bytes(1, K, N)
-        reps += 1
-        if time.perf_counter() - t0 > budget_s or reps >= 5:
-            break
-    elapsed = t_deq + t_mm
+            td += m - a
+            tm += e - m
+        if r:   # the first pass warms up
+            deq.append(td)
+            mm.append(tm)
+    return _median(deq) * 1e3, _median(mm) * 1e3
+
+
+def cpu_baseline(device):
+    """The reference's CPU path (numpy dequant + fp32 BLAS matmul, the oracle's restatement
+    of tools/convert.py:82-89 and kernels/linear.metal:4) on every BASELINE config, on this
+    host: dequant (single-threaded numpy) and matmul (multi-threaded BLAS) timed apart, the
+    median of several runs after a warm-up (bounded samples where a config is large, as
+    each entry says). The headline entry is config 2's layer at M = 1 (q/k/v stacked)."""
+    import numpy as np
+    import torch
+
+    from raceline_amd import synth
+    from raceline_amd.configs import CFG1_SINGLE, CFG2_9B_STACKED, CFG3_27B, CFG4_PREFILL_M, MOE, linear_bytes
+
+    threads, model = blas_threads(), cpu_model()
+    table = {}
+
+    def layer(name, shapes, Ms, runs, seed):
+        mats = [_host_affine(device, K, N, seed + i) for i, (_, K, N) in enumerate(shapes)]
+        for M in Ms:
+            xs = [synth.random_activations(M, K, seed + 50 + i, device, 0.01 if M > 8 else 0.0).cpu().numpy()
+                  for i, (_, K, _) in enumerate(shapes)]
+            d, m = _cpu_linear(mats, xs, runs)
+            nbytes = sum(linear_bytes(M, K, N) for _, K, N in shapes)
+            flops = sum(2 * M * K * N for _, K, N in shapes)
+            table[f"{name}_m{M}"] = {"dequant_ms": round(d, 2), "matmul_ms": round(m, 2), "total_ms": round(d + m, 2),
+                                     "GB/s": round(nbytes / (d + m) / 1e6, 3),
+                                     "TFLOP/s": round(flops / (d + m) / 1e9, 4), "runs": runs}
+            log(f"[bench] CPU {name} M={M}: dequant {d:.1f} ms + matmul {m:.1f} ms")
+        del mats
+
+    layer("cfg1_single", CFG1_SINGLE, (1,), 5, 4200)
+    layer("cfg2_9b_layer", CFG2_9B_STACKED, (1, 5), 5, 4242)
+    layer("cfg3_27b_layer", CFG3_27B, (1, 8), 3, 4300)
+    layer("cfg4_27b_prefill", CFG3_27B, (CFG4_PREFILL_M,), 2, 4300)
+    # config 5: the MoE layer restated on the host (route, then each expert's dequant and its
+    # rows' gate/up, SwiGLU, down), at T = 1 and, for T = 512, a sample of 32 of the experts
+    # with their routed rows, scaled to all of them
+    E, H, I, topk = MOE["E"], MOE["H"], MOE["I"], MOE["topk"]
+    gu = _host_affine(device, H, (E + 1) * 2 * I, 4400)
+    dn = _host_affine(device, I, (E + 1) * H, 4401)
+    import oracle as O
+    for T in MOE["tokens"]:
+        x = synth.random_activations(T, H, 4402 + T, device).cpu().numpy()
+        g = torch.Generator(device=device)
+        g.manual_seed(4403 + T)
+        logits = torch.randn((T, E + 1), generator=g, device=device, dtype=torch.float32).cpu().numpy()
+        sel, _ = O.moe_route(logits, E, topk)
+        experts = sorted(set(int(e) for e in sel))
+        sample = experts if T == 1 else experts[:: max(1, len(experts) // 32)][:32]
+        rows_of = {e: [a // (topk + 1) for a in range(len(sel)) if int(sel[a]) == e] for e in sample}
+        deq, mm = [], []
+        for r in range(4):
+            td = tm = 0.0
+            for e in sample:
+                a = time.perf_counter()
+                rg, rd = slice(e * 2 * I, (e + 1) * 2 * I), slice(e * H, (e + 1) * H)
+                Wg = O.dequant_affine(O.unpack_nibbles_u32(gu[0][rg]), gu[1][rg], gu[2][rg], "f16")
+                Wd = O.dequant_affine(O.unpack_nibbles_u32(dn[0][rd]), dn[1][rd], dn[2][rd], "f16")
+                m = time.perf_counter()
+                gg = x[rows_of[e]].astype(np.float32) @ Wg.T
+                act = (gg[:, :I] / (1 + np.exp(-gg[:, :I])) * gg[:, I:]).astype(np.float16)
+                _ = act.astype(np.float32) @ Wd.T
+                f = time.perf_counter()
+                td += m - a
+                tm += f - m
+            if r:
+                deq.append(td * len(experts) / len(sample))
+                mm.append(tm * len(experts) / len(sample))
+        d, m = _median(deq) * 1e3, _median(mm) * 1e3
+        table[f"cfg5_moe_t{T}"] = {"dequant_ms": round(d, 2), "matmul_ms": round(m, 2), "total_ms": round(d + m, 2),
+                                   "experts": len(experts), "experts_timed": len(sample), "runs": 3}
+        log(f"[bench] CPU MoE T={T}: dequant {d:.1f} ms + matmul {m:.1f} ms ({len(sample)} of {len(experts)} experts)")
+    del gu, dn
+    head = table["cfg2_9b_layer_m1"]
     return {
-        "value": total_bytes / elapsed / 1e9, "unit": "GB/s", "cores": int(blas_threads), "kind": "port",
-        "sample": f"9B decode layer (6 projections, q/k/v stacked) at M=1, {reps} passes: numpy unpack+dequant "
-                  f"(1 thread) {t_deq / reps * 1e3:.1f} ms + fp32 BLAS matmul ({blas_threads} threads) "
-                  f"{t_mm / reps * 1e3:.1f} ms per layer; host has {os.cpu_count()} logical CPUs",
-        "ms_per_layer": elapsed / reps * 1e3,
+        "value": head["GB/s"], "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": (f"config 2 layer (q/k/v stacked, o, gate_up, down) at M=1: numpy unpack+dequant (1 thread) "
+                   f"{head['dequant_ms']} ms + fp32 BLAS matmul ({threads} threads) {head['matmul_ms']} ms, "
+                   f"median of {head['runs']} after a warm-up; host: {model}, {os.cpu_count()} logical CPUs; "
+                   f"every config under detail.cpu_baseline_per_config"),
+        "cpu_model": model, "per_config": table,
     }
 
 
@@ -489,7 +620,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail configs, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--part", choices=["prefill", "moe", "decode"],
+    ap.add_argument("--part", choices=["prefill", "moe", "decode", "epilogue", "cpu"],
                     help="run only this part of the detail (for rocprofv3); prints its figures as JSON")
     ap.add_argument("--profile", action="store_true",
                     help="launch only the dominant kernel and a calibration kernel (for rocprofv3)")
@@ -503,6 +634,11 @@ def main():
 
     if args.profile:
         profile_dominant(max(args.steps, 40))
+        return
+    if args.part == "cpu":
+        import torch
+
+        print(json.dumps(cpu_baseline(torch.device("cuda:0"))), flush=True)
         return
     if args.part:
         print(json.dumps(bench_part(args.part, args.steps, args.warmup)), flush=True)
@@ -577,6 +713,7 @@ def main():
         # prefill: M = 2048, compute bound; two copies are plenty
         detail.update(bench_prefill(dev, args.steps, args.warmup))
         detail.update(bench_moe(dev, args.steps, args.warmup))
+        detail.update(bench_native_epilogue(dev, args.steps, args.warmup))
 
     cpu = None
     if not args.quick and not args.no_cpu:
@@ -593,11 +730,12 @@ def main():
                                "fp16 scales+biases, M=1, fp32 accumulate", "global_batch": 1, "seq_len": 1,
                    "parallelism": "single GPU", "weight_copies": copies, "bytes_per_step": bytes1},
         "roofline": roofline,
-        "cpu_baseline": None if cpu is None else {k: v for k, v in cpu.items() if k != "ms_per_layer"},
+        "cpu_baseline": None if cpu is None else {k: v for k, v in cpu.items() if k != "per_config"},
         "detail": detail,
     }
     if cpu is not None:
         line["cpu_baseline"]["value"] = round(cpu["value"], 3)
+        detail["cpu_baseline_per_config"] = cpu["per_config"]
     print(json.dumps(line), flush=True)
 
 

@@ -134,6 +134,13 @@ int rlq_linear_native_kernel(int kernel, const void *x, int x_stride, int M, int
                              const float *s_row, int book, float *y, int y_stride, int accum, void *workspace,
                              size_t workspace_bytes, void *stream);
 
+/* y[m][n] = sum_k x[m][k] * L[q[n][k]]: the native product without the row scale (or any
+ * other epilogue), as linear_q4n_raw computes it to measure what linear_q4n's epilogue costs
+ * (kernels/linear.metal:226-252). book RLQ_BOOK_INT15 or RLQ_BOOK_FP4 (that kernel's W_T has
+ * no half step); other arguments as rlq_linear_native. */
+int rlq_linear_native_raw(const void *x, int x_stride, int M, int K, int N, const void *packed, int book, float *y,
+                          int y_stride, void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------- dense fp16 linear */
 
 /* Half-precision matrices (the MoE router, the MTP head's input projection) in MFMA

@@ -27,6 +27,13 @@ def moe_route(logits, E: int, topk: int, norm_topk: bool = True):
     norm_topk (:92-102). Slot topk is the shared expert (number E) with weight
     sigmoid(logit[E]) (:103-104).
 
+    One deliberate difference: when a row has fewer than topk finite logits, the reference's
+    rounds go on picking the lowest-numbered expert whose value is -inf (:75-91), which can
+    be an expert already chosen (chosen ones are set to -inf), so it repeats experts. This
+    restatement, like the HIP kernels, takes distinct experts (the remaining ones in index
+    order): the sort's per-token ranking needs distinct experts. The weights of those slots
+    are exp(-inf) = 0 in both, so h is the same; sel, tok and items differ.
+
     Returns (sel [T*S] int, w [T*S] float64), S = topk + 1, in (token, slot) order."""
     L = np.asarray(logits, dtype=np.float32)
     T = L.shape[0]

@@ -442,7 +442,7 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   // D of a 32x32 tile: lane l holds column l%32, rows 8 (v/4) + 4 (l/32) + v%4
   const int n = n0 + 32 * wave + c32;
   if (n >= a.N) return;
-  const float rs_n = BOOK == kAffine ? 1.0f : a.srow[n];
+  const float rs_n = BOOK == kAffine || !a.srow ? 1.0f : a.srow[n];   // no row scales: the raw product
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll

@@ -306,7 +306,7 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
   // lane (c16, j4) holds token rows 4 j4 .. 4 j4 + 3 of output n
   if constexpr (MAXM == 1) acc = reduce_waves(acc, red, wave, waves, lane);
   if (wave == 0 && n < a.N && 4 * j4 < M) {
-    const float rs = BOOK == kAffine ? 1.0f : a.srow[n];
+    const float rs = BOOK == kAffine || !a.srow ? 1.0f : a.srow[n];   // no row scales: the raw product
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = 4 * j4 + v;
@@ -371,7 +371,7 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
   for (int h = 0; h < 2; ++h) {
     const int n = 16 * (t0 + h) + c16;
     if (n >= a.N) continue;
-    const float rs = BOOK == kAffine ? 1.0f : a.srow[n];
+    const float rs = BOOK == kAffine || !a.srow ? 1.0f : a.srow[n];   // no row scales: the raw product
     const f32x4 &acc = h ? acc1 : acc0;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -623,6 +623,16 @@ int rlq_linear_native_kernel(int kernel, const void *x, int x_stride, int M, int
   // native matrices have no scale/bias section: the codes stand in for it (never read)
   return linear_packed(kernel, book, static_cast<const _Float16 *>(x), x_stride, M, K, N, packed, packed, RLQ_F16,
                        s_row, y, y_stride, accum, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int rlq_linear_native_raw(const void *x, int x_stride, int M, int K, int N, const void *packed, int book, float *y,
+                          int y_stride, void *workspace, size_t workspace_bytes, void *stream) {
+  int rc = check_linear_args("rlq_linear_native_raw", x, x_stride, M, K, N, packed, RLQ_F16, y, y_stride);
+  if (rc) return rc;
+  RLQ_REQUIRE(book == RLQ_BOOK_INT15 || book == RLQ_BOOK_FP4,
+              "rlq_linear_native_raw: codebook %d (int15 or fp4: the raw product has no half step)", book);
+  return linear_packed(0, book, static_cast<const _Float16 *>(x), x_stride, M, K, N, packed, packed, RLQ_F16, nullptr,
+                       y, y_stride, 0, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int rlq_linear_native(const void *x, int x_stride, int M, int K, int N, const void *packed, const float *s_row,

@@ -44,6 +44,8 @@ SIGNATURES = {
                                   c_int, c_void_p, c_size_t, c_void_p]),
     "rlq_linear_native_kernel": (c_int, [c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int,
                                          c_void_p, c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "rlq_linear_native_raw": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int,
+                                      c_void_p, c_size_t, c_void_p]),
     "rlq_packed_f16_bytes": (c_size_t, [c_int, c_int]),
     "rlq_pack_f16": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "rlq_pack_f16_blocked": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),

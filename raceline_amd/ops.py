@@ -181,6 +181,21 @@ def linear_native(x: torch.Tensor, nw: NativeWeight, out: torch.Tensor | None = 
     return out
 
 
+def linear_native_raw(x: torch.Tensor, nw: NativeWeight, out: torch.Tensor | None = None,
+                      kernel_stream=None) -> torch.Tensor:
+    """out[m][n] = sum_k x[m][k] * L[q[n][k]]: the native product without the row scale
+    (rlq_linear_native_raw; int15 and fp4 only)."""
+    if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < nw.K:
+        raise ValueError("x must be a row-major float16 [M][>= K] matrix")
+    M, K, N = x.shape[0], nw.K, nw.N
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    ws = _WS.get(x.device, workspace_bytes(M, K, N))
+    lib.call("rlq_linear_native_raw", _ptr(x), x.stride(0), M, K, N, _ptr(nw.packed), nw.code, _ptr(out),
+             out.stride(0), _ptr(ws), 0 if ws is None else ws.numel(), _stream(kernel_stream))
+    return out
+
+
 @dataclass
 class DenseWeight:
     """A half-precision matrix [N][K] in MFMA operand order (rlq_pack_f16)."""

@@ -103,3 +103,8 @@ def test_no_alloc_moe_refuses_sizes_past_its_scratch():
     assert L.rlq_moe_workspace_bytes(4096, 256, 8, 2048, 512) > cap
     with pytest.raises(lib.RlqError, match="more than the 50331648 it holds"):
         lib.call("rlq_moe_no_alloc", 16, 2048, 16, 257, 4096, 256, 8, 1, 2048, 512, 16, 16, 0, 16, 2048, None)
+
+
+def test_raw_native_product_refuses_the_half_step_book():
+    with pytest.raises(lib.RlqError, match="no half step"):
+        lib.call("rlq_linear_native_raw", 16, 64, 1, 64, 16, 16, 2, 16, 16, None, 0, None)

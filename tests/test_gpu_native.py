@@ -134,3 +134,23 @@ def test_native_reads_nothing_past_the_weight(gpu, book):
         y = _run(gpu, x, nw2, kernel=kernel)
         assert np.isfinite(y).all(), f"kernel {kernel} read past the packed codes"
         O.check_close(y, O.linear_native_f64(x, q, s_row, book), TOL, f"native tail {book} kernel {kernel}")
+
+
+@pytest.mark.parametrize("book", ["int15", "fp4"])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 1024), (5, 12288, 512), (64, 2048, 300)])
+def test_raw_product(gpu, book, M, K, N):
+    """rlq_linear_native_raw (linear_q4n_raw, kernels/linear.metal:226-252): the product
+    without the row scale. It equals the scaled product with unit row scales bit for bit
+    (the epilogue multiplies by 1), and the fp64 product x . L(q)^T."""
+    import torch
+
+    from raceline_amd import ops
+
+    rng = np.random.default_rng(M + K)
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    x = rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)
+    raw = ops.linear_native_raw(to_dev(x, gpu), _upload(q, rng.uniform(0.5, 2, N), book, gpu))
+    unit = ops.linear_native(to_dev(x, gpu), _upload(q, np.ones(N, np.float32), book, gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(raw, unit)
+    O.check_close(raw.cpu().numpy(), O.linear_native_f64(x, q, np.ones(N), book), TOL, f"raw {book} M={M}")

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the 4-bit quantized matmul path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu] [--profile]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu] [--profile [gemv|moe]]
 
 Headline (BASELINE metric "4-bit GEMV achieved HBM GB/s at M=1"): one step is the
 9B-class decode layer's six projections (q, k, v, o, gate_up, down)
@@ -601,6 +601,46 @@ def profile_dominant(launches):
         f"calibration: 10 x torch.neg over {CALIBRATION_BYTES >> 20} MiB")
 
 
+def profile_moe(launches, T=512):
+    """--profile moe: the MoE layer (H=2048, E=256 + shared, I=512, top-8) at T tokens,
+    launched eagerly over rotating copies of the experts (each step routes, multiplies and
+    combines: moe_topk, moe_sort, the gate/up and down expert kernels, moe_combine), then
+    the calibration kernel of profile_dominant. Meant to run under rocprofv3 --pmc."""
+    import torch
+
+    from raceline_amd import lib, ops, synth
+    from raceline_amd.configs import MOE
+
+    lib.load()
+    dev = torch.device("cuda:0")
+    E, H, I, topk = MOE["E"], MOE["H"], MOE["I"], MOE["topk"]
+    per_copy = ops.packed_bytes(H, (E + 1) * 2 * I) + ops.packed_bytes(I, (E + 1) * H)
+    copies = max(2, -(-CACHE_DEFEAT_BYTES // per_copy))
+    mws = []
+    for c in range(copies):
+        gu = synth.random_affine((E + 1) * 2 * I, H, 500 + 2 * c, dev, packed=False)
+        dn = synth.random_affine((E + 1) * H, I, 501 + 2 * c, dev, packed=False)
+        mws.append(ops.pack_moe(gu, dn, E, H, I))
+        del gu, dn
+    x = synth.random_activations(T, H, 600 + T, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(601 + T)
+    logits = torch.randn((T, E + 1), generator=g, device=dev, dtype=torch.float32)
+    h = torch.zeros((T, H), dtype=torch.float32, device=dev)
+    ws = torch.empty(ops.moe_workspace_bytes(T, E, topk, H, I), dtype=torch.uint8, device=dev)
+    for i in range(launches):
+        ops.moe(x, logits, mws[i % copies], topk, h, workspace=ws)
+    torch.cuda.synchronize()
+    distinct = int(torch.unique(ops.moe_route(logits, E, topk).sel).numel())
+    a = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(10):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    log(f"[profile] MoE T={T}: {launches} layer steps over {copies} copies of {per_copy / 1e6:.1f} MB, "
+        f"{distinct} distinct experts; calibration: 10 x torch.neg over {CALIBRATION_BYTES >> 20} MiB")
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter
     summary (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration kernel), or None."""
@@ -622,8 +662,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--part", choices=["prefill", "moe", "decode", "epilogue", "cpu"],
                     help="run only this part of the detail (for rocprofv3); prints its figures as JSON")
-    ap.add_argument("--profile", action="store_true",
-                    help="launch only the dominant kernel and a calibration kernel (for rocprofv3)")
+    ap.add_argument("--profile", nargs="?", const="gemv", choices=["gemv", "moe"],
+                    help="launch only the dominant kernel (gemv) or the MoE layer at T=512 (moe), eagerly, "
+                         "and a calibration kernel (for rocprofv3 --pmc)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -632,8 +673,11 @@ def main():
               "sharding is a design only); run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
-    if args.profile:
+    if args.profile == "gemv":
         profile_dominant(max(args.steps, 40))
+        return
+    if args.profile == "moe":
+        profile_moe(max(args.steps, 20))
         return
     if args.part == "cpu":
         import torch

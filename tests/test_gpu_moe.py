@@ -137,7 +137,8 @@ def test_gate_up_swiglu_and_down(gpu, sd):
 
 
 @pytest.mark.parametrize("T,E,topk,H,I", [(1, 16, 4, 256, 128), (33, 32, 4, 512, 256), (5, 256, 8, 2048, 512),
-                                           (4, 64, 8, 512, 512), (2, 16, 4, 256, 1024)])
+                                           (4, 64, 8, 512, 512), (2, 16, 4, 256, 1024),
+                                           (70, 32, 4, 512, 256), (130, 16, 4, 320, 192)])
 def test_layer_matches_oracle(gpu, T, E, topk, H, I):
     import torch
 
@@ -214,13 +215,16 @@ def test_layer_full_size_batch_invariance(gpu):
     O.check_close(h.cpu().numpy()[toks].astype(np.float64), ref, TOL, "moe full-size sampled tokens")
 
 
-@pytest.mark.parametrize("E,H,I", [(64, 2048, 512), (16, 1024, 1536), (16, 1536, 1024), (16, 4096, 256)])
+@pytest.mark.parametrize("E,H,I", [(64, 2048, 512), (16, 1024, 1536), (16, 1536, 1024), (16, 4096, 256),
+                                   (32, 576, 320)])
 def test_token_result_same_across_kernel_choice(gpu, E, H, I):
     """Calls of fewer than 8 tokens run the per-tile expert kernel, larger ones the kernel
     that stages each item's rows in LDS; a token's result must not depend on which one
-    ran: tokens 3..7 alone (per-tile) give the same bits as inside a 40-token call. The
-    shapes cover K (H for gate/up, I for down) where the staged kernel's waves take one
-    (512, 1024, 4096) and two (1536, 2048) of the per-tile kernel's group ranges."""
+    ran or on how many tokens share an expert: tokens 3..7 alone (per-tile) and the first
+    40 give the same bits as inside a 100-token call.
+    The shapes cover K (H for gate/up, I for down) where the staged kernel's waves take
+    one (512, 1024, 4096) and two (1536, 2048) of the per-tile kernel's group ranges, and
+    odd group counts (576 = 9 groups, 320 = 5)."""
     import torch
 
     from raceline_amd import ops
@@ -228,9 +232,11 @@ def test_token_result_same_across_kernel_choice(gpu, E, H, I):
     topk = 8
     gu, dn = make_moe(90, E, H, I)
     mw = upload_moe(gu, dn, E, H, I, "f16", gpu)
-    x, logits = make_inputs(91, 40, E, H)
-    h = torch.zeros((40, H), dtype=torch.float32, device=gpu)
+    x, logits = make_inputs(91, 100, E, H)
+    h = torch.zeros((100, H), dtype=torch.float32, device=gpu)
     ops.moe(to_dev(x, gpu), to_dev(logits, gpu), mw, topk, h)
+    h40 = torch.zeros((40, H), dtype=torch.float32, device=gpu)
+    ops.moe(to_dev(x[:40].copy(), gpu), to_dev(logits[:40].copy(), gpu), mw, topk, h40)
     h5 = torch.zeros((5, H), dtype=torch.float32, device=gpu)
     ops.moe(to_dev(x[3:8].copy(), gpu), to_dev(logits[3:8].copy(), gpu), mw, topk, h5)
     # up to 4 tokens also fold the combine into the down launch; one token also routes in
@@ -240,6 +246,7 @@ def test_token_result_same_across_kernel_choice(gpu, E, H, I):
     h1 = torch.zeros((1, H), dtype=torch.float32, device=gpu)
     ops.moe(to_dev(x[7:8].copy(), gpu), to_dev(logits[7:8].copy(), gpu), mw, topk, h1)
     _sync()
+    assert torch.equal(h40, h[:40])
     assert torch.equal(h5, h[3:8])
     assert torch.equal(h3, h[3:6])
     assert torch.equal(h1, h[7:8])

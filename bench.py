@@ -377,6 +377,63 @@ def bench_decode(device, steps, warmup):
     return out
 
 
+def bench_launch_cost(device, steps, warmup):
+    """The decode kernel's cost per launch at K = 4096 (BASELINE config 1 is N = 4096): the
+    average kernel time of back-to-back launches in a captured graph over rotating weight
+    copies (>= 1 GiB, so every launch streams from HBM) for N = 512 ... 49152, and the
+    straight line t = t0 + bytes / rate fitted to the N >= 4096 points by least squares:
+    t0 is what a launch costs beyond streaming its bytes (dispatch, the first loads'
+    latency, the last wave's reduction and stores). Also the time of a launch that does
+    next to nothing (torch's fill of one float) in the same kind of graph."""
+    import torch
+
+    from raceline_amd import synth
+    from raceline_amd.configs import linear_bytes
+
+    K = 4096
+    rows = []
+    for N in (512, 1024, 2048, 4096, 8192, 16384, 24576, 49152):
+        per = linear_bytes(1, K, N)
+        copies = max(2, min(512, -(-CACHE_DEFEAT_BYTES // per)))
+        shapes = [("w", K, N)]
+        layers = [[synth.random_affine(N, K, 7 + c, device)] for c in range(copies)]
+        launches = max(copies, 64)
+        t = time_kernel(layers, shapes, 1, 0, device, launches=launches)
+        rows.append((N, per, t))
+        log(f"[bench] decode launch K={K} N={N}: {t * 1e6:.2f} us, {per / t / 1e9:.0f} GB/s ({copies} copies)")
+        del layers
+        torch.cuda.empty_cache()
+    fit = [(b, t) for N, b, t in rows if N >= 4096]
+    n = len(fit)
+    mb = sum(b for b, _ in fit) / n
+    mt = sum(t for _, t in fit) / n
+    slope = sum((b - mb) * (t - mt) for b, t in fit) / sum((b - mb) ** 2 for b, _ in fit)
+    t0 = mt - slope * mb
+    # a launch of almost no work, in a graph of back-to-back launches on one stream
+    one = torch.zeros(1, device=device)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(256):
+            one.fill_(1.0)
+    with torch.cuda.stream(stream):
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+    t_empty = e0.elapsed_time(e1) / 1e3 / 256
+    log(f"[bench] fit over N >= 4096: t0 = {t0 * 1e6:.2f} us per launch, stream rate {1 / slope / 1e9:.0f} GB/s; "
+        f"fill of one float: {t_empty * 1e6:.2f} us per launch")
+    return {"K": K, "points": [{"N": N, "bytes": b, "us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+                               for N, b, t in rows],
+            "fit_t0_us": round(t0 * 1e6, 2), "fit_stream_GBps": round(1 / slope / 1e9, 1),
+            "empty_launch_us": round(t_empty * 1e6, 2)}
+
+
 def bench_part(part, steps, warmup):
     import torch
 
@@ -385,7 +442,8 @@ def bench_part(part, steps, warmup):
     lib.load()
     dev = torch.device("cuda:0")
     log(f"[bench] part {part}")
-    fn = {"prefill": bench_prefill, "moe": bench_moe, "decode": bench_decode, "epilogue": bench_native_epilogue}[part]
+    fn = {"prefill": bench_prefill, "moe": bench_moe, "decode": bench_decode, "epilogue": bench_native_epilogue,
+          "launch": bench_launch_cost}[part]
     return fn(dev, steps, warmup)
 
 
@@ -660,7 +718,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail configs, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--part", choices=["prefill", "moe", "decode", "epilogue", "cpu"],
+    ap.add_argument("--part", choices=["prefill", "moe", "decode", "epilogue", "launch", "cpu"],
                     help="run only this part of the detail (for rocprofv3); prints its figures as JSON")
     ap.add_argument("--profile", nargs="?", const="gemv", choices=["gemv", "moe"],
                     help="launch only the dominant kernel (gemv) or the MoE layer at T=512 (moe), eagerly, "

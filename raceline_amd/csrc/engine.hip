@@ -397,6 +397,7 @@ static int open_engine(rl_engine *e, const char *path, int max_ctx, int max_chun
     if (int rc = dev_alloc(e->proj, R * e->proj_stride * 4, "proj")) return rc;
   if (int rc = dev_alloc(e->act, R * std::max(e->act_stride, 8) * 2 + 256, "act")) return rc;
   if (int rc = dev_alloc(e->linear_ws, lin_ws, "the linear workspace")) return rc;
+  if (lin_ws) RLQ_HIP(hipMemset(e->linear_ws.p, 0, lin_ws));   // the decode kernel's split counters start at zero
   if (c.is_moe()) {
     const QTensor *router = e->model->q(lname(0, "moe.router"));
     RLQ_REQUIRE(router, "model has no quantized tensor '%s'", lname(0, "moe.router").c_str());

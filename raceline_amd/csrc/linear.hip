@@ -185,6 +185,17 @@ __global__ void dequant_kernel(const u32x4 *codes, const u32x4 *sb, int K, int N
 // every weight load of a wave is issued before its first multiply.
 //
 // The operand trick and the MFMA group sums are described in q4_tile.h.
+//
+// Split of K across workgroups (split_of): a weight with few tiles and a long K (the
+// down projections: 320 tiles of 272 groups at 27B) leaves most CUs one workgroup or
+// none, and its loads cannot fill the chip. There, the grid is (tiles, S): workgroup
+// (t, s) takes groups [s * gsplit, (s + 1) * gsplit) of tile t, stores its partial sums
+// in the workspace as agent-scope atomic stores, waits for them to complete and adds one
+// to the tile's counter (an agent-scope atomic); the workgroup that brings the counter to
+// S reads the S partials back (agent-scope atomic loads, issued after its increment
+// returned), adds them in split order 0, 1, ... from zero, writes y and sets the counter
+// back to zero. No workgroup waits for another. The split depends on K and N only, so a
+// token's result is the same whatever other tokens share the call.
 constexpr int kGemvMaxM = 8;
 struct GemvArgs {
   const _Float16 *x;
@@ -193,7 +204,25 @@ struct GemvArgs {
   const float *srow;    // native books: the scale of each output row
   float *y;
   int x_stride, M, K, N, y_stride;
+  int split, gsplit;    // K split: S workgroups per tile, gsplit groups each (S = 1: none)
+  float *part;          // S > 1: partial sums [S][M][N]
+  int *cnt;             // S > 1: arrivals per tile (zero between calls)
 };
+
+// The workspace's first kGemvCountBytes hold the split counters (zero before the first
+// call; every call leaves them zero); the partials and the prefill kernel's data follow.
+constexpr size_t kGemvCountBytes = 4096;
+// S for a weight: 4 where the tiles are few (4 tiles <= 1280 workgroups) and each split
+// keeps at least 64 groups, else 1. The hand-over costs a few microseconds of latency at
+// the end (partials out, the count, partials back), which pays where K is long: measured
+// on the 27B down (K = 17408, N = 5120) at M = 1, 16.2 -> 13.3 us; on the 9B down
+// (K = 12288, N = 4096) a split in 2 lost (7.5 -> 8.9 us).
+constexpr int kSplit = 4;
+static int split_of(int K, int N) {
+  const int G = K / kGroup, tiles = tiles_of(N);
+  return (long long)tiles * kSplit <= 1280 && G / kSplit >= 64 ? kSplit : 1;
+}
+static int gsplit_of(int K, int S) { return ((K / kGroup + S - 1) / S + 3) / 4 * 4; }
 
 // Groups per wave: the smallest of 8, 12, 16, 24 that needs at most 16 waves. Smaller
 // ranges put more waves (and more loads) in flight per tile; below 8 the per-wave setup
@@ -204,10 +233,15 @@ static int gemv_gpw(int K) {
   return g <= 8 * 16 ? 8 : g <= 12 * 16 ? 12 : g <= 16 * 16 ? 16 : 24;
 }
 static int gemv_waves(int K) { const int g = gemv_gpw(K); return (4 * quads_of(K) + g - 1) / g; }
+// the K a workgroup covers: all of K, or one split's groups
+static int gemv_k_per_wg(int K, int N) {
+  const int S = split_of(K, N);
+  return S == 1 ? K : gsplit_of(K, S) * kGroup;
+}
 // The automatic choice takes the decode kernel for M <= 8 when its 16 waves cover K
 // (K <= 24576); longer reductions at decode sizes go to the prefill kernel, which takes
 // any K.
-static bool decode_fits(int M, int K) { return M <= kGemvMaxM && gemv_waves(K) <= 16; }
+static bool decode_fits(int M, int K, int N) { return M <= kGemvMaxM && gemv_waves(gemv_k_per_wg(K, N)) <= 16; }
 
 // M = 1: the cross-wave reduction [waves-1][64][4] floats, then each wave's staged
 // activations [gpw * 64] halves. M > 1: each wave's staged rows, M * kStagedXRow bytes
@@ -215,6 +249,57 @@ static bool decode_fits(int M, int K) { return M <= kGemvMaxM && gemv_waves(K) <
 static size_t gemv_lds_bytes(int M, int waves, int gpw) {
   if (M > 1) return (size_t)waves * M * kStagedXRow;
   return (size_t)(waves - 1) * 64 * 16 + (size_t)waves * gpw * kGroup * 2;
+}
+
+// The end of a split workgroup (see split_of), in the wave holding its NT tiles' sums
+// (tiles t0 .. t0 + NT - 1, arrivals counted on counter c): stores the partials, counts
+// the arrival and returns false, except in the tile's last workgroup, where acc[h] becomes
+// the sum of the S partials in split order and true is returned.
+template <int NT>
+__device__ __forceinline__ bool split_arrive(const GemvArgs &a, int c, int t0, f32x4 (&acc)[NT], int lane) {
+  const int M = a.M, c16 = lane & 15, j4 = lane >> 4;
+  float *part = a.part + (size_t)blockIdx.y * M * a.N;
+#pragma unroll
+  for (int h = 0; h < NT; ++h) {
+    const int n = 16 * (t0 + h) + c16;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * j4 + v;
+      if (n < a.N && m < M)
+        __hip_atomic_store(part + (size_t)m * a.N + n, acc[h][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);                // the partials are stored before the count
+  int old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(a.cnt + c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readfirstlane(old);    // lane 0's: every lane is active again here
+  if (old != kSplit - 1) return false;          // uniform: the tile's last workgroup goes on
+  // every partial is requested before the first is added (one wait for all of them); the
+  // lanes past M or N read a stored partial (their row and column clamped) and drop it
+  float p[kSplit][NT][4];
+#pragma unroll
+  for (int q = 0; q < kSplit; ++q)
+#pragma unroll
+    for (int h = 0; h < NT; ++h) {
+      const int n = min(16 * (t0 + h) + c16, a.N - 1);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = min(4 * j4 + v, M - 1);
+        p[q][h][v] = __hip_atomic_load(a.part + ((size_t)q * M + m) * a.N + n, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+#pragma unroll
+  for (int h = 0; h < NT; ++h)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kSplit; ++q) sum += p[q][h][v];
+      acc[h][v] = sum;
+    }
+  if (lane == 0) __hip_atomic_store(a.cnt + c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
 }
 
 // MAXM: 1 (single-token decode: one activation row, one live accumulator) or 8.
@@ -233,10 +318,12 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
   const int M = a.M;
   f32x4 *red = reinterpret_cast<f32x4 *>(lds);                              // [waves-1][64]
 
-  // this wave's groups [wg0, wg0 + GPW) of tile t; wn of them are real
-  const int wg0 = wave * GPW;
-  const int wn = max(0, min(G, wg0 + GPW) - wg0);
-  const WaveTile wt = wave_tile(a.codes, a.sb, t, G4, wg0, GPW);
+  // this wave's groups [wg0, wg0 + GPW) of tile t within its split's [g_lo, g_hi); wn of
+  // them are real (the loads stop at the split's end, rounded up to a quad)
+  const int g_lo = blockIdx.y * a.gsplit, g_hi = min(G, g_lo + a.gsplit);
+  const int wg0 = g_lo + wave * GPW;
+  const int wn = max(0, min(g_hi, wg0 + GPW) - wg0);
+  const WaveTile wt = wave_tile(a.codes, a.sb, t, G4, wg0, wn > 0 ? min(GPW, (wn + 3) / 4 * 4) : 0);
   const uint32_t xrange = wn > 0 ? (uint32_t)((M - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
 
@@ -305,6 +392,12 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
 
   // lane (c16, j4) holds token rows 4 j4 .. 4 j4 + 3 of output n
   if constexpr (MAXM == 1) acc = reduce_waves(acc, red, wave, waves, lane);
+  if (a.split > 1) {
+    if (wave != 0) return;
+    f32x4 accs[1] = {acc};
+    if (!split_arrive<1>(a, t, t, accs, lane)) return;
+    acc = accs[0];
+  }
   if (wave == 0 && n < a.N && 4 * j4 < M) {
     const float rs = BOOK == kAffine || !a.srow ? 1.0f : a.srow[n];   // no row scales: the raw product
 #pragma unroll
@@ -339,10 +432,12 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
   const int t0 = 2 * blockIdx.x, t1 = t0 + 1;
   const int M = a.M;
 
-  const int wg0 = wave * GPW;
-  const int wn = max(0, min(G, wg0 + GPW) - wg0);
-  const WaveTile w0 = wave_tile(a.codes, a.sb, t0, G4, wg0, GPW);
-  const WaveTile w1 = wave_tile(a.codes, a.sb, min(t1, tiles - 1), G4, wg0, t1 < tiles ? GPW : 0);
+  const int g_lo = blockIdx.y * a.gsplit, g_hi = min(G, g_lo + a.gsplit);   // the split's groups
+  const int wg0 = g_lo + wave * GPW;
+  const int wn = max(0, min(g_hi, wg0 + GPW) - wg0);
+  const int wl = wn > 0 ? min(GPW, (wn + 3) / 4 * 4) : 0;                   // loads stop at the split's end
+  const WaveTile w0 = wave_tile(a.codes, a.sb, t0, G4, wg0, wl);
+  const WaveTile w1 = wave_tile(a.codes, a.sb, min(t1, tiles - 1), G4, wg0, t1 < tiles ? wl : 0);
   const uint32_t xrange = wn > 0 ? (uint32_t)((M - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
   // LDS: wave w's staged activation rows at w * M * kStagedXRow; once the wave is done with
@@ -357,7 +452,7 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
     reinterpret_cast<f32x4 *>(xs)[64 + lane] = acc1;
   }
   __syncthreads();
-  if (wave != 0 || 4 * j4 >= M) return;
+  if (wave != 0) return;
   for (int w = 1; w < waves; ++w) {
     const f32x4 *red = reinterpret_cast<const f32x4 *>(lds + (size_t)w * M * kStagedXRow);
     const f32x4 o0 = red[lane], o1 = red[64 + lane];
@@ -367,6 +462,13 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
       acc1[v] += o1[v];
     }
   }
+  if (a.split > 1) {
+    f32x4 accs[2] = {acc0, acc1};
+    if (!split_arrive<2>(a, blockIdx.x, t0, accs, lane)) return;
+    acc0 = accs[0];
+    acc1 = accs[1];
+  }
+  if (4 * j4 >= M) return;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int n = 16 * (t0 + h) + c16;
@@ -385,7 +487,11 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
   }
 }
 
-static size_t gemv_workspace(int, int, int) { return 0; }
+// the partials of a split weight (the counters sit in the workspace's first kGemvCountBytes)
+static size_t gemv_workspace(int M, int K, int N) {
+  const int S = split_of(K, N);
+  return S == 1 ? 0 : (size_t)S * std::min(M, kGemvMaxM) * N * 4;
+}
 
 // PAIR: the two-tile kernel (M > 1 only).
 template <int MAXM, int GPW, int SD, bool ACC, int BOOK, bool PAIR>
@@ -428,10 +534,17 @@ static int launch_gemv(int book, int sd, int accum, dim3 grid, int threads, size
 // book: kAffine (packed holds codes then scale/bias quads; sd their dtype) or a native
 // codebook (packed holds codes only; srow the row scales).
 static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes, const void *sbq,
-                    int sd, const float *srow, float *y, int y_stride, int accum, hipStream_t st) {
+                    int sd, const float *srow, float *y, int y_stride, int accum, int *cnt, float *part,
+                    size_t part_bytes, hipStream_t st) {
   RLQ_REQUIRE(M <= kGemvMaxM, "decode kernel handles M <= %d rows (got %d)", kGemvMaxM, M);
-  const int gpw = gemv_gpw(K), waves = gemv_waves(K);
+  const int S = split_of(K, N), kw = gemv_k_per_wg(K, N);
+  const int gpw = gemv_gpw(kw), waves = gemv_waves(kw);
   RLQ_REQUIRE(waves <= 16, "decode kernel: K=%d is larger than the %d it supports", K, 16 * 24 * kGroup);
+  if (S > 1)
+    RLQ_REQUIRE(cnt && part && part_bytes >= gemv_workspace(M, K, N),
+                "decode kernel: K=%d N=%d splits K in %d and needs rlq_linear_workspace_bytes(%d, %d, %d) = %zu bytes "
+                "of workspace (got %zu)", K, N, S, M, K, N, kGemvCountBytes + gemv_workspace(M, K, N),
+                part_bytes + (cnt ? kGemvCountBytes : 0));
   const size_t lds = gemv_lds_bytes(M, waves, gpw);
   GemvArgs a;
   a.x = x;
@@ -440,7 +553,11 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
   a.srow = srow;
   a.y = y;
   a.x_stride = x_stride; a.M = M; a.K = K; a.N = N; a.y_stride = y_stride;
-  const dim3 grid(tiles_of(N));
+  a.split = S;
+  a.gsplit = S == 1 ? K / kGroup : gsplit_of(K, S);
+  a.part = S == 1 ? nullptr : part;
+  a.cnt = S == 1 ? nullptr : cnt;
+  const dim3 grid(tiles_of(N), S);
   const int threads = 64 * waves;
   int rc;
   if (M == 1) rc = gpw == 8    ? launch_gemv<1, 8>(book, sd, accum, grid, threads, lds, st, a)
@@ -448,7 +565,7 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
                    : gpw == 16 ? launch_gemv<1, 16>(book, sd, accum, grid, threads, lds, st, a)
                                : launch_gemv<1, 24>(book, sd, accum, grid, threads, lds, st, a);
   else if (gpw == 8)   // two tiles per workgroup, activations staged in LDS
-    rc = launch_gemv<kGemvMaxM, 8, true>(book, sd, accum, dim3((tiles_of(N) + 1) / 2), threads, lds, st, a);
+    rc = launch_gemv<kGemvMaxM, 8, true>(book, sd, accum, dim3((tiles_of(N) + 1) / 2, S), threads, lds, st, a);
   else rc = gpw == 12 ? launch_gemv<kGemvMaxM, 12>(book, sd, accum, grid, threads, lds, st, a)
             : gpw == 16 ? launch_gemv<kGemvMaxM, 16>(book, sd, accum, grid, threads, lds, st, a)
                         : launch_gemv<kGemvMaxM, 24>(book, sd, accum, grid, threads, lds, st, a);
@@ -461,9 +578,16 @@ int linear_packed(int kernel, int book, const _Float16 *x, int x_stride, int M, 
                   const void *sbq, int sd, const float *srow, float *y, int y_stride, int accum, void *ws,
                   size_t ws_bytes, hipStream_t st) {
   RLQ_REQUIRE(kernel >= 0 && kernel <= 2, "unknown kernel %d", kernel);
-  const bool gemv = kernel == 1 || (kernel == 0 && decode_fits(M, K));
-  if (gemv) return run_gemv(book, x, x_stride, M, K, N, codes, sbq, sd, srow, y, y_stride, accum, st);
-  return run_gemm4(book, x, x_stride, M, K, N, codes, sbq, sd, srow, y, y_stride, accum, ws, ws_bytes, st);
+  // the workspace: split counters first, then the decode partials or the prefill kernel's data
+  const bool has_ws = ws && ws_bytes >= kGemvCountBytes;
+  int *cnt = has_ws ? static_cast<int *>(ws) : nullptr;
+  void *rest = has_ws ? static_cast<char *>(ws) + kGemvCountBytes : nullptr;
+  const size_t rest_bytes = has_ws ? ws_bytes - kGemvCountBytes : 0;
+  const bool gemv = kernel == 1 || (kernel == 0 && decode_fits(M, K, N));
+  if (gemv)
+    return run_gemv(book, x, x_stride, M, K, N, codes, sbq, sd, srow, y, y_stride, accum, cnt,
+                    static_cast<float *>(rest), rest_bytes, st);
+  return run_gemm4(book, x, x_stride, M, K, N, codes, sbq, sd, srow, y, y_stride, accum, rest, rest_bytes, st);
 }
 
 // ================================================================== group sums
@@ -644,9 +768,10 @@ int rlq_linear_native(const void *x, int x_stride, int M, int K, int N, const vo
 
 size_t rlq_linear_workspace_bytes(int M, int K, int N) {
   if (M <= 0 || K <= 0 || N <= 0 || K % kGroup) return 0;
-  // the largest of the books (the affine prefill kernel's prepped activations)
-  return std::max({M <= kGemvMaxM ? gemv_workspace(M, K, N) : (size_t)0, gemm4_workspace(kAffine, M, K, N),
-                   gemm4_workspace(kInt16, M, K, N), gemm4_workspace(kInt15, M, K, N)});
+  // the split counters, then the largest of the decode partials (up to 8 rows: a workspace
+  // sized for M serves every smaller M) and the books' prefill data
+  return kGemvCountBytes + std::max({gemv_workspace(std::min(M, kGemvMaxM), K, N), gemm4_workspace(kAffine, M, K, N),
+                                     gemm4_workspace(kInt16, M, K, N), gemm4_workspace(kInt15, M, K, N)});
 }
 
 int rlq_linear_affine_kernel(int kernel, const void *x, int x_stride, int M, int K, int N, const void *packed,

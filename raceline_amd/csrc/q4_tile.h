@@ -116,13 +116,14 @@ __device__ __forceinline__ float fma_scale(uint32_t pr, float p, float acc) {
 }
 
 // Descriptors over one wave's part of one 16-row tile: groups [wg0, wg0 + GPW) of tile t.
-// Loads past the wave's part (padding groups, the next wave's range) return zeros.
+// Loads past the wave's part (padding groups, the next wave's range) return zeros; a wave
+// whose range starts past the tile's groups gets empty descriptors.
 struct WaveTile {
   __amdgpu_buffer_rsrc_t rw, rs;
 };
 
 __device__ __forceinline__ WaveTile wave_tile(const u32x4 *codes, const u32x4 *sb, int t, int G4, int wg0, int gpw) {
-  const int wq1 = min(4 * G4, wg0 + gpw);
+  const int wq1 = max(wg0, min(4 * G4, wg0 + gpw));
   WaveTile w;
   w.rw = make_rsrc(codes + ((size_t)t * 2 * G4 + wg0 / 2) * 64, (uint32_t)(wq1 - wg0) / 2u * 1024u);
   w.rs = make_rsrc(sb + ((size_t)t * G4 + wg0 / 4) * 16, (uint32_t)(wq1 - wg0) / 4u * 256u);

@@ -234,8 +234,10 @@ def linear_f16(x: torch.Tensor, dw: DenseWeight, out: torch.Tensor | None = None
 
 
 class _Workspaces:
-    """One scratch buffer per device, grown on demand (its contents are not kept between
-    calls). Calls that use it must not overlap on two streams of one device."""
+    """One scratch buffer per device, grown on demand, zero-filled when allocated (the
+    decode kernel keeps its split counters at the start of the linear workspace and leaves
+    them zero after every call; nothing else is kept between calls). Calls that use it
+    must not overlap on two streams of one device."""
 
     def __init__(self):
         self._bufs = {}
@@ -248,7 +250,7 @@ class _Workspaces:
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
-                buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 

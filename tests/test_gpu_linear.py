@@ -141,6 +141,28 @@ def test_gemm_rows_do_not_depend_on_other_rows(gpu, K, N):
     np.testing.assert_array_equal(y_sub, y_all[50:120])
 
 
+@pytest.mark.parametrize("K,N", [(16384, 512), (16448, 40), (17408, 1000)])   # K split in 4; 257 groups; ragged N
+def test_split_k_decode_between_other_calls(gpu, K, N):
+    """Weights whose K the decode kernel splits across workgroups (few tiles, long K) keep
+    their arrival counters in the workspace's first bytes and leave them zero: a split call,
+    a prefill call that fills the same workspace with its own data, a split call of other
+    rows, and a split call with ACCUM all match the oracle; one row alone gives the same
+    bits as inside M = 8."""
+    q, s, b = make_layer(21 + K, N, K)
+    wt = upload(q, s, b, "f16", gpu)
+    x8 = make_x(22, 8, K)
+    ref8 = O.linear_affine_f64(x8, q, s, b)
+    y8 = _run(gpu, x8, wt, kernel=1)
+    O.check_close(y8, ref8, TOL, f"split gemv M=8 K={K} N={N}")
+    xg = make_x(23, 64, K)
+    O.check_close(_run(gpu, xg, wt, kernel=2), O.linear_affine_f64(xg, q, s, b), TOL, "gemm on the same workspace")
+    for m in (0, 5, 7):
+        np.testing.assert_array_equal(_run(gpu, x8[m:m + 1], wt, kernel=1)[0], y8[m])
+    y0 = np.random.default_rng(24).standard_normal((3, N)).astype(np.float32)
+    y = _run(gpu, x8[:3], wt, kernel=1, accum_into=y0)
+    O.check_close(y, ref8[:3] + y0, TOL, "split gemv accum")
+
+
 def test_repeat_calls_reuse_workspace(gpu):
     """Repeated calls give identical results (no state carried between calls)."""
     M, K, N = 1, 4096, 1024
@@ -253,7 +275,8 @@ def test_reference_correctness_cases(gpu, M, K, N):
         O.check_close(y[:, cols], ref, TOL, f"reference case M={M} K={K} N={N} via {name}")
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 17408, 40), (5, 17408, 40), (1, 640, 48), (3, 2560, 33)])
+@pytest.mark.parametrize("M,K,N", [(1, 17408, 40), (5, 17408, 40), (1, 640, 48), (3, 2560, 33),
+                                   (1, 16448, 40), (8, 16448, 40)])   # K split in 4, the last split short
 def test_gemv_reads_nothing_past_the_weight(gpu, M, K, N):
     """A wave's last groups past K (K not a multiple of its group range) must read zeros,
     not whatever follows the packed weight in memory: the weight sits at the head of a

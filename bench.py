@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the 4-bit quantized matmul path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu] [--profile [gemv|moe]]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu] [--profile [gemv|moe|gemm]]
 
 Headline (BASELINE metric "4-bit GEMV achieved HBM GB/s at M=1"): one step is the
 9B-class decode layer's six projections (q, k, v, o, gate_up, down)
@@ -699,6 +699,34 @@ def profile_moe(launches, T=512):
         f"{distinct} distinct experts; calibration: 10 x torch.neg over {CALIBRATION_BYTES >> 20} MiB")
 
 
+def profile_gemm(launches):
+    """--profile gemm: the prefill kernel alone on the 27B gate_up (M = 2048, K = 5120,
+    N = 34816, activations with 1% outliers x20), launched eagerly over two weight copies,
+    then the calibration kernel of profile_dominant. Meant to run under rocprofv3 --pmc."""
+    import torch
+
+    from raceline_amd import lib, ops, synth
+    from raceline_amd.configs import CFG3_27B, CFG4_PREFILL_M
+
+    lib.load()
+    dev = torch.device("cuda:0")
+    _, K, N = [c for c in CFG3_27B if c[0] == "gate_up"][0]
+    M = CFG4_PREFILL_M
+    ws = [synth.random_affine(N, K, 1 + 1000 * c, dev) for c in range(2)]
+    x = synth.random_activations(M, K, 99, dev, 0.01)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    for i in range(launches):
+        ops.linear(x, ws[i % 2], out=y)
+    torch.cuda.synchronize()
+    a = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(10):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    log(f"[profile] gemm4 M={M} K={K} N={N}: {launches} launches over 2 copies; "
+        f"calibration: 10 x torch.neg over {CALIBRATION_BYTES >> 20} MiB")
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter
     summary (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration kernel), or None."""
@@ -720,9 +748,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--part", choices=["prefill", "moe", "decode", "epilogue", "launch", "cpu"],
                     help="run only this part of the detail (for rocprofv3); prints its figures as JSON")
-    ap.add_argument("--profile", nargs="?", const="gemv", choices=["gemv", "moe"],
-                    help="launch only the dominant kernel (gemv) or the MoE layer at T=512 (moe), eagerly, "
-                         "and a calibration kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--profile", nargs="?", const="gemv", choices=["gemv", "moe", "gemm"],
+                    help="launch only the dominant kernel (gemv), the MoE layer at T=512 (moe) or the prefill "
+                         "kernel on the 27B gate_up (gemm), eagerly, and a calibration kernel (for rocprofv3 --pmc)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -736,6 +764,9 @@ def main():
         return
     if args.profile == "moe":
         profile_moe(max(args.steps, 20))
+        return
+    if args.profile == "gemm":
+        profile_gemm(max(min(args.steps, 20), 6))
         return
     if args.part == "cpu":
         import torch

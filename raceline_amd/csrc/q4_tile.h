@@ -71,7 +71,9 @@ __device__ __forceinline__ half8 nib8_to_half8_sub(uint32_t u) {
   d[0] = u & 0x000F000Fu;
   d[1] = (u >> 4) & 0x000F000Fu;
   d[2] = (u >> 8) & 0x000F000Fu;
-  d[3] = (u >> 12) & 0x000F000Fu;
+  // the top nibble of each 16-bit half: one packed 16-bit shift clears the rest (six ops
+  // in all instead of seven; the same bits)
+  d[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, u) >> (u16x2){12, 12});
   return __builtin_bit_cast(half8, d);
 }
 

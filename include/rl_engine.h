@@ -109,6 +109,14 @@ int rl_draft_tail(const rl_engine *e);
 int rl_draft_vocab(const rl_engine *e);
 size_t rl_logits_stride(const rl_engine *e);
 
+/* src/capi.h:79-83: the expert cache of a mixture of experts kept on disk. This engine
+ * keeps every expert resident in device memory, so it has none: rl_expert_cache returns 0
+ * slots with *hits = *loads = 0, and rl_expert_cache_size gives 0 experts of 0 bytes, as
+ * the reference reports for an engine without a cache (src/engine.mm:364-365). Null
+ * pointers are allowed. */
+int rl_expert_cache(const rl_engine *e, unsigned long long *hits, unsigned long long *loads);
+void rl_expert_cache_size(const rl_engine *e, int *experts, unsigned long long *slot_bytes);
+
 /* The head over the draft vocabulary for one row of h (the logits part of
  * Engine::encode_mtp_layer, src/engine.mm:1419-1436): final norm, lm_head rows
  * [0, rl_draft_main()) and, when a tail is set, rows [rl_draft_tail(), n_pad) right after

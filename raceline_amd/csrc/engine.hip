@@ -652,6 +652,22 @@ int rl_draft_vocab(const rl_engine *e) {
   return rl_draft_main(e) + (tail < 0 ? 0 : head->n_pad - tail);
 }
 
+// Every expert of a mixture of experts stays resident in HBM (288 GB holds the largest
+// MoE file whole), so there is no expert cache: as src/engine.mm:364-365 reports for an
+// engine without one, no slots, no hits or loads, and a size of zero.
+int rl_expert_cache(const rl_engine *e, unsigned long long *hits, unsigned long long *loads) {
+  (void)e;
+  if (hits) *hits = 0;
+  if (loads) *loads = 0;
+  return 0;
+}
+
+void rl_expert_cache_size(const rl_engine *e, int *experts, unsigned long long *slot_bytes) {
+  (void)e;
+  if (experts) *experts = 0;
+  if (slot_bytes) *slot_bytes = 0;
+}
+
 size_t rl_logits_stride(const rl_engine *e) {
   const QTensor *head = e ? e->model->q("lm_head") : nullptr;
   return head ? (size_t)head->n_pad : 0;

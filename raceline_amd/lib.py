@@ -91,6 +91,8 @@ SIGNATURES = {
     "rl_draft_tail": (c_int, [c_void_p]),
     "rl_draft_vocab": (c_int, [c_void_p]),
     "rl_logits_stride": (c_size_t, [c_void_p]),
+    "rl_expert_cache": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "rl_expert_cache_size": (None, [c_void_p, c_void_p, c_void_p]),
     "rl_draft_head": (c_void_p, [c_void_p, c_void_p, c_void_p]),
     "rl_top_k": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "rl_top_k_device": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),

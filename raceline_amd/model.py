@@ -176,6 +176,23 @@ class Engine:
     def draft_vocab(self) -> int:
         return int(lib.load().rl_draft_vocab(self._e))
 
+    def expert_cache(self):
+        """(slots, hits, loads) of the expert cache, or None when every expert is in memory
+        (raceline/engine.py:262-267); this engine keeps them all in HBM."""
+        hits, loads = ctypes.c_ulonglong(), ctypes.c_ulonglong()
+        slots = lib.load().rl_expert_cache(self._e, ctypes.byref(hits), ctypes.byref(loads))
+        return (slots, hits.value, loads.value) if slots else None
+
+    def expert_cache_size(self):
+        """(GB the cache holds, share of the experts that fit in it), or None when every
+        expert is in memory (raceline/engine.py:269-276)."""
+        slots = lib.load().rl_expert_cache(self._e, None, None)
+        if not slots:
+            return None
+        n, size = ctypes.c_int(), ctypes.c_ulonglong()
+        lib.load().rl_expert_cache_size(self._e, ctypes.byref(n), ctypes.byref(size))
+        return slots * size.value / 1e9, slots / max(1, n.value)
+
     def draft_head(self, h_row: torch.Tensor) -> torch.Tensor:
         ptr = lib.load().rl_draft_head(self._e, h_row.data_ptr(), _stream())
         if not ptr:

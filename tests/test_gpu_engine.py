@@ -15,11 +15,14 @@ writer, against the oracle:
   rl_argmax give rl_top_k's ids and values exactly.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
 import oracle as O
 import oracle.engine as OE
+from raceline_amd import lib
 from raceline_amd.model import Engine, top_k
 from tests import model_files as MF
 from tests.qdata import to_dev
@@ -170,6 +173,11 @@ def test_moe_mlp(gpu, tmp_path, book):
                 e.mlp(0, one)
                 _sync()
                 assert torch.equal(one[0], h[1])
+        # every expert is resident: no expert cache, as the reference reports without one
+        assert e.expert_cache() is None and e.expert_cache_size() is None
+        hits, loads = ctypes.c_ulonglong(7), ctypes.c_ulonglong(7)
+        assert lib.load().rl_expert_cache(e._e, ctypes.byref(hits), ctypes.byref(loads)) == 0
+        assert hits.value == 0 and loads.value == 0
 
 
 @pytest.mark.parametrize("book", BOOKS)

@@ -29,6 +29,7 @@
 #include "../../include/rlq.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace rlq {
 
@@ -40,6 +41,13 @@ constexpr int kBBytes = (kGN / 16) * 1024;  // stage part: the 16 tiles' code ki
 constexpr int kSBytes = (kGN / 16) * 256;   // stage part: their scale/bias quads, 4 KB
 constexpr int kStageBytes = kABytes + kBBytes + kSBytes;
 constexpr int kStages = 3;                  // loads run two group pairs ahead of the MFMAs
+constexpr int kGroupM = 4;                  // token blocks per group of the workgroup order
+// LDS by part, then stage: the three activation tiles, the three code parts, the three
+// scale parts, so that with the stage known at compile time every read of a stage is a
+// lane's base address plus an immediate offset
+constexpr int a_part(int stage) { return stage * kABytes; }
+constexpr int b_part(int stage) { return kStages * kABytes + stage * kBBytes; }
+constexpr int s_part(int stage) { return kStages * (kABytes + kBBytes) + stage * kSBytes; }
 
 // ------------------------------------------------------------------ affine prep pass
 
@@ -164,8 +172,8 @@ struct StageSrc {
   int K, GP, G4, wave, lane;
 };
 
-__device__ __forceinline__ __attribute__((address_space(3))) void *lds_at(unsigned char *lds, int stage, int off) {
-  return (__attribute__((address_space(3))) void *)(lds + (size_t)stage * kStageBytes + off);
+__device__ __forceinline__ __attribute__((address_space(3))) void *lds_at(unsigned char *lds, int off) {
+  return (__attribute__((address_space(3))) void *)(lds + off);
 }
 
 // Loads group pair p into LDS stage `stage`: 4 activation chunks (16 bytes each), 2 code
@@ -179,7 +187,7 @@ __device__ __forceinline__ void issue_stage(const StageSrc &s, unsigned char *ld
   if (128 * (p + 1) <= s.K) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, stage, (4 * s.wave + i) * 1024), 16, s.a_off[i],
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, a_part(stage) + (4 * s.wave + i) * 1024), 16, s.a_off[i],
                                                256 * p, 0, 0);
   } else {
 #pragma unroll
@@ -187,35 +195,34 @@ __device__ __forceinline__ void issue_stage(const StageSrc &s, unsigned char *ld
       const int r = 4 * (4 * s.wave + i) + (s.lane >> 4);
       const int c = (s.lane & 15) ^ (r & 15);
       const bool ok = s.a_row[i] && 128 * p + 8 * c < s.K;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, stage, (4 * s.wave + i) * 1024), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, a_part(stage) + (4 * s.wave + i) * 1024), 16,
                                                ok ? s.a_off[i] + (uint32_t)(256 * p) : kFarOffset, 0, 0, 0);
     }
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int k = 2 * s.wave + i;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rcode, lds_at(lds, stage, kABytes + k * 1024), 16,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rcode, lds_at(lds, b_part(stage) + k * 1024), 16,
                                              (uint32_t)k * s.GP * 1024u + 16u * s.lane, p * 1024, 0, 0);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int k = 2 * s.wave + i;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rsb, lds_at(lds, stage, kABytes + kBBytes + k * 256), 4,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rsb, lds_at(lds, s_part(stage) + k * 256), 4,
                                              (uint32_t)k * s.G4 * 256u + 4u * s.lane, (p >> 1) * 256, 0, 0);
   }
 }
 
 
 // The B reads of a pair (two 16-byte code slots) and, affine, its two scale words.
-template <int BOOK>
-__device__ __forceinline__ void read_pair_head(const unsigned char *lds, uint32_t boff, uint32_t soff, int stage,
-                                               int p, u32x4 (&wq)[2], uint32_t (&sp)[2]) {
-  const unsigned char *base = lds + (size_t)stage * kStageBytes;
-  wq[0] = *reinterpret_cast<const u32x4 *>(base + boff);
-  wq[1] = *reinterpret_cast<const u32x4 *>(base + boff + 512);
+template <int BOOK, int STAGE>
+__device__ __forceinline__ void read_pair_head(const unsigned char *lds, uint32_t boff, uint32_t soff, int p,
+                                               u32x4 (&wq)[2], uint32_t (&sp)[2]) {
+  wq[0] = *reinterpret_cast<const u32x4 *>(lds + b_part(STAGE) + boff);
+  wq[1] = *reinterpret_cast<const u32x4 *>(lds + b_part(STAGE) + boff + 512);
   if constexpr (BOOK == kAffine) {
     typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-    const u32x2 v = *reinterpret_cast<const u32x2 *>(base + soff + 8 * (p & 1));
+    const u32x2 v = *reinterpret_cast<const u32x2 *>(lds + s_part(STAGE) + soff + 8 * (p & 1));
     sp[0] = v[0];
     sp[1] = v[1];
   }
@@ -224,9 +231,10 @@ __device__ __forceinline__ void read_pair_head(const unsigned char *lds, uint32_
 
 // A fragment of step j of a pair (see gemm4_kernel): token tile 2 ((j >> 3) & 1) + (j & 1),
 // 32 rows of 256 bytes apart per tile, chunk of step (j >> 1) & 3 of group j >> 4.
-__device__ __forceinline__ half8 read_frag(const unsigned char *lds, int stage, const uint32_t (&aoff)[2][4], int j) {
+template <int STAGE>
+__device__ __forceinline__ half8 read_frag(const unsigned char *lds, const uint32_t (&aoff)[2][4], int j) {
   const int gg = j >> 4, mt = 2 * ((j >> 3) & 1) + (j & 1), i = (j >> 1) & 3;
-  return *reinterpret_cast<const half8 *>(lds + (size_t)stage * kStageBytes + mt * 32 * kARowBytes + aoff[gg][i]);
+  return *reinterpret_cast<const half8 *>(lds + a_part(STAGE) + mt * 32 * kARowBytes + aoff[gg][i]);
 }
 
 template <int BOOK, int SD, bool ACC>
@@ -249,14 +257,17 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   const bool acc_here = ACC && split == 0;
 
   // Workgroups are numbered round-robin over the 8 XCDs; give each XCD a contiguous
-  // range of tiles, token blocks fastest, so the workgroups of one XCD share feature
-  // blocks (weights) in its L2.
+  // range of tiles, ordered in groups of kGroupM token blocks (token blocks fastest, then
+  // feature blocks), so the workgroups an XCD runs at once share both their activation
+  // rows and their weights in its L2 (kGroupM 4: 4 token x 8 feature blocks per XCD).
   const int nwg = gridDim.x, wid = blockIdx.x;
   const int per_xcd = (nwg + 7) / 8;
   int lin = (wid % 8) * per_xcd + wid / 8;
   if (nwg % 8 != 0) lin = wid;                      // uneven grids keep the plain order
-  const int mblocks = (a.M + kGM - 1) / kGM;
-  const int mb = lin % mblocks, nb = lin / mblocks;
+  const int mblocks = (a.M + kGM - 1) / kGM, nblocks = (a.N + kGN - 1) / kGN;
+  const int group = lin / (kGroupM * nblocks), first_m = group * kGroupM;
+  const int gm = min(mblocks - first_m, kGroupM), rem = lin - group * kGroupM * nblocks;
+  const int mb = first_m + rem % gm, nb = rem / gm;
   const int m0 = mb * kGM, n0 = nb * kGN;
 
   // Every stage of the LDS ring holds, for one group pair: the activation tile (rows with
@@ -299,8 +310,8 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   for (int gg = 0; gg < 2; ++gg)
 #pragma unroll
     for (int i = 0; i < 4; ++i) aoff[gg][i] = (uint32_t)(c32 * kARowBytes + (((8 * gg + 2 * i + h) ^ cr) << 4));
-  const uint32_t boff = (uint32_t)(kABytes + kt * 1024 + 256 * h + 16 * cr);
-  const uint32_t soff = (uint32_t)(kABytes + kBBytes + kt * 256 + 16 * cr);
+  const uint32_t boff = (uint32_t)(kt * 1024 + 256 * h + 16 * cr);   // within a stage's code part
+  const uint32_t soff = (uint32_t)(kt * 256 + 16 * cr);               // within its scale part
 
   // The K loop is software-pipelined over the 32 MFMAs of a group pair, in a fixed order:
   // step j = 16 gg + 8 half + 2 i + t multiplies token tile mt = 2 half + t by the codes of
@@ -331,12 +342,14 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0F78);                     // vmcnt(8): stage 0 in place, 1 may fly
   asm volatile("s_barrier" ::: "memory");
   issue_stage(src, lds, pb + min(2, NPs - 1), 2);
-  read_pair_head<BOOK>(lds, boff, soff, 0, pb, wq, sp);
+  read_pair_head<BOOK, 0>(lds, boff, soff, pb, wq, sp);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) carry[j] = read_frag(lds, 0, aoff, j);
+  for (int j = 0; j < 8; ++j) carry[j] = read_frag<0>(lds, aoff, j);
 
-  for (int q = 0; q < NPs; ++q) {
-    const int stage = q % kStages;
+  // Pair q from stage STAGE = q % 3. The loop below runs the pairs three at a time, so the
+  // stage of every LDS read is a compile-time constant.
+  auto pair = [&](auto stage_c, int q) {
+    constexpr int STAGE = decltype(stage_c)::value, NEXT = (STAGE + 1) % kStages;
     const bool more = q + 1 < NPs;
     half8 fr[32];
 #pragma unroll
@@ -351,13 +364,13 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
         // and stage p + 1 has landed for every wave
         __builtin_amdgcn_s_waitcnt(0x0078);                   // lgkmcnt(0) vmcnt(8): stage p + 2 may fly
         asm volatile("s_barrier" ::: "memory");
-        issue_stage(src, lds, pb + min(q + 3, NPs - 1), (q + 3) % kStages);
+        issue_stage(src, lds, pb + min(q + 3, NPs - 1), STAGE);   // (q + 3) % 3 == STAGE
         // the last codes of this pair were read at step 22
-        read_pair_head<BOOK>(lds, boff, soff, (q + 1) % kStages, pb + q + 1, wq, sp);
+        read_pair_head<BOOK, NEXT>(lds, boff, soff, pb + q + 1, wq, sp);
       }
       // (past the last pair the carried reads see a stale stage, and are not used)
-      if (j + 8 < 32) fr[j + 8] = read_frag(lds, stage, aoff, j + 8);
-      else carry[j - 24] = read_frag(lds, (q + 1) % kStages, aoff, j - 24);
+      if (j + 8 < 32) fr[j + 8] = read_frag<STAGE>(lds, aoff, j + 8);
+      else carry[j - 24] = read_frag<NEXT>(lds, aoff, j - 24);
       if ((j & 15) == 0 && BOOK == kAffine) sc = scale_f32<SD>((uint16_t)(sp[gg] & 0xFFFFu)) * kTwo24;
       if ((j & 15) < 8 && t == 0) {
         // codes of step i, group gg: word 2i + h, i.e. read (i & 1), element 2 gg + (i >> 1)
@@ -387,7 +400,15 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  int q = 0;
+  for (; q + kStages <= NPs; q += kStages) {
+    pair(std::integral_constant<int, 0>{}, q);
+    pair(std::integral_constant<int, 1>{}, q + 1);
+    pair(std::integral_constant<int, 2>{}, q + 2);
   }
+  if (q < NPs) pair(std::integral_constant<int, 0>{}, q);
+  if (q + 1 < NPs) pair(std::integral_constant<int, 1>{}, q + 1);
   __builtin_amdgcn_s_waitcnt(0);                          // the clamped duplicates have landed
   if constexpr (BOOK == kAffine) {
 #pragma unroll

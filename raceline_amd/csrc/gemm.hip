@@ -42,6 +42,7 @@ constexpr int kSBytes = (kGN / 16) * 256;   // stage part: their scale/bias quad
 constexpr int kStageBytes = kABytes + kBBytes + kSBytes;
 constexpr int kStages = 3;                  // loads run two group pairs ahead of the MFMAs
 constexpr int kGroupM = 4;                  // token blocks per group of the workgroup order
+constexpr int kBiasChunk = 32;              // bias product: steps of group-sum pieces staged at a time
 // LDS by part, then stage: the three activation tiles, the three code parts, the three
 // scale parts, so that with the stage known at compile time every read of a stage is a
 // lane's base address plus an immediate offset
@@ -423,39 +424,65 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
     // pieces (gemm_prep_kernel). Step st covers k' = 16 st .. +15; lane half h holds k'
     // 16 st + 8 h .. +7: for fp16 biases (P = 2) the (hi, lo) of groups 8 st + 4 h .. +3, so
     // b of those groups, each twice; for bf16 biases (P = 4) the pieces of groups
-    // 4 st + 2 h and + 1, so b of those two, four times each. The scale quads come
-    // straight from memory.
+    // 4 st + 2 h and + 1, so b of those two, four times each. Every wave needs the pieces of
+    // all 128 rows, so they go through the LDS, which the ring no longer uses: LDS-DMA'd
+    // once per workgroup, kBiasChunk steps at a time, rows padded by 16 bytes (an odd
+    // number of 16-byte slots apart, so the fragment reads of 32 rows spread over the
+    // banks). Each wave's scale quads (its own biases) come straight from memory, in flight
+    // while the pieces land.
     const int tn = t0 + 2 * wave;
     const int tv = max(0, min(T, tn + 2) - tn);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sb + (size_t)min(tn, T) * G4 * 16, (uint32_t)tv * G4 * 256u);
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.gs, (uint32_t)((size_t)a.M * a.gs_stride * 2));
     const int steps = a.gs_stride / 16;
-    for (int st = 0; st < steps; ++st) {
-      const int q = SD == 0 ? 2 * st + h : st;       // quad of groups 4q .. 4q+3
-      const u32x4 v = q < G4 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             rs, (uint32_t)tt * G4 * 256u + (uint32_t)q * 256u + 16u * cr, 0, 0))
-                             : u32x4{};
-      u32x4 d;
-      if constexpr (SD == 0) {
+    for (int st0 = 0; st0 < steps; st0 += kBiasChunk) {
+      const int cs = min(kBiasChunk, steps - st0);
+      const int rowb = 32 * cs + 16;                       // LDS bytes per row
+      u32x4 v[kBiasChunk];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) d[e] = (v[e] >> 16) * 0x10001u;           // (b, b): times hi and lo
-      } else {
-        const uint32_t b0 = (h ? v[2] : v[0]) >> 16, b1 = (h ? v[3] : v[1]) >> 16;
-        d[0] = d[1] = b0 * 0x10001u;                                           // b of group 4q + 2h, four times
-        d[2] = d[3] = b1 * 0x10001u;                                           // and of group 4q + 2h + 1
+      for (int u = 0; u < kBiasChunk; ++u) {
+        const int q = SD == 0 ? 2 * (st0 + u) + h : st0 + u;   // quad of groups 4q .. 4q+3
+        v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rs, u < cs && q < G4 ? (uint32_t)tt * G4 * 256u + (uint32_t)q * 256u + 16u * cr
+                                                                  : kFarOffset,
+                                             0, 0));
       }
+      __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0): this wave's LDS reads are done
+      asm volatile("s_barrier" ::: "memory");               // and every wave's
+      // 1 KB blocks of the chunk (128 rows of rowb bytes), each lane 16 bytes; pad slots and
+      // rows past M read zeros
+      const int nblk = (kGM * rowb + 1023) / 1024;
+      for (int blk = wave; blk < nblk; blk += kGThreads / 64) {
+        const int pos = blk * 1024 + 16 * lane, row = pos / rowb, col = pos - row * rowb;
+        const bool ok = row < kGM && col < 32 * cs && m0 + row < a.M;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rg, lds_at(lds, blk * 1024), 16,
+            ok ? (uint32_t)(((size_t)(m0 + row) * a.gs_stride + 16 * st0) * 2 + col) : kFarOffset, 0, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0);                        // the pieces (and the scale quads) landed
+      asm volatile("s_barrier" ::: "memory");
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const int m = m0 + mt * 32 + c32;
-        const u32x4 ag = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rg, m < a.M ? (uint32_t)(((size_t)m * a.gs_stride + 16 * st + 8 * h) * 2) : kFarOffset, 0, 0));
-        if constexpr (SD == 0)
-          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, ag), __builtin_bit_cast(half8, d),
-                                                          acc[mt], 0, 0, 0);
-        else
-          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ag),
-                                                           __builtin_bit_cast(bf16x8, d), acc[mt], 0, 0, 0);
+      for (int u = 0; u < kBiasChunk; ++u) {
+        if (u >= cs) continue;                              // uniform
+        u32x4 d;
+        if constexpr (SD == 0) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) d[e] = (v[u][e] >> 16) * 0x10001u;       // (b, b): times hi and lo
+        } else {
+          const uint32_t b0 = (h ? v[u][2] : v[u][0]) >> 16, b1 = (h ? v[u][3] : v[u][1]) >> 16;
+          d[0] = d[1] = b0 * 0x10001u;                                         // b of group 4q + 2h, four times
+          d[2] = d[3] = b1 * 0x10001u;                                         // and of group 4q + 2h + 1
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const u32x4 ag = *reinterpret_cast<const u32x4 *>(lds + (mt * 32 + c32) * rowb + 32 * u + 16 * h);
+          if constexpr (SD == 0)
+            acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, ag),
+                                                            __builtin_bit_cast(half8, d), acc[mt], 0, 0, 0);
+          else
+            acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ag),
+                                                             __builtin_bit_cast(bf16x8, d), acc[mt], 0, 0, 0);
+        }
       }
     }
   }

@@ -89,6 +89,97 @@ __device__ __forceinline__ uint32_t bf16_rne_bits(float v) {   // finite v
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// The pieces of one group sum of the scaled row (see kGsPieces), and the zero padding of the
+// row's pieces up to gs_stride after its last group.
+template <int SD>
+__device__ __forceinline__ void write_gs_pieces(uint16_t *gs, int gs_stride, int m, int g, int G, float sum) {
+  constexpr int P = kGsPieces<SD>;
+  uint16_t *dst = gs + (size_t)m * gs_stride + P * g;
+  if constexpr (SD == 0) {
+    const _Float16 hi = static_cast<_Float16>(sum);
+    const _Float16 lo = static_cast<_Float16>(sum - static_cast<float>(hi));
+    dst[0] = __builtin_bit_cast(uint16_t, hi);
+    dst[1] = __builtin_bit_cast(uint16_t, lo);
+  } else {
+    const uint32_t hi = bf16_rne_bits(sum);
+    const float r1 = sum - __uint_as_float(hi << 16);         // exact
+    const uint32_t mid = bf16_rne_bits(r1);
+    const uint32_t lo = bf16_rne_bits(r1 - __uint_as_float(mid << 16));   // exact: 8 bits remain
+    dst[0] = (uint16_t)hi;
+    dst[1] = (uint16_t)mid;
+    dst[2] = (uint16_t)lo;
+    dst[3] = 0;
+  }
+  if (g == G - 1)   // the row's padding up to gs_stride is zero (no memset: this runs in graphs)
+    for (int k = P * G; k < gs_stride; ++k) gs[(size_t)m * gs_stride + k] = 0;
+}
+
+// The workgroup's max |x| of its row from each thread's partial max.
+__device__ __forceinline__ float row_max(float mx, float *wmax) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, d));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kPrepThreads / 64; ++w) mx = __builtin_fmaxf(mx, wmax[w]);
+  return mx;
+}
+
+// 2^e for the row's largest magnitude (max |x| 2^e in [2^8, 2^9)); 1 for a row that is all
+// zeros or holds an infinity or a NaN.
+__device__ __forceinline__ int row_exponent(float mx) {
+  int ex = 0;
+  if (mx > 0.0f && mx <= 65504.0f) {
+    int k;
+    (void)__builtin_frexpf(mx, &k);                     // mx = f 2^k, f in [0.5, 1)
+    ex = 9 - k;                                         // mx 2^ex in [2^8, 2^9)
+  }
+  return ex;
+}
+
+// The prep pass with the row read once: thread i holds chunks i, i + 256, ... (CPT of
+// them, K <= 2048 CPT) in registers between the max and the writes. The same arithmetic in
+// the same order as gemm_prep_kernel below, so the same bits.
+template <int SD, int CPT>
+__global__ __launch_bounds__(kPrepThreads) void gemm_prep1_kernel(const _Float16 *x, int x_stride, int M, int K,
+                                                                  _Float16 *xp, uint16_t *gs, int gs_stride,
+                                                                  float *rscale) {
+  __shared__ float wmax[kPrepThreads / 64];
+  const int m = blockIdx.x;
+  const int C = K / 8;                                  // chunks per row (a multiple of 8)
+  const _Float16 *row = x + (size_t)m * x_stride;
+  u32x4 v[CPT];
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = threadIdx.x + kPrepThreads * j;
+    v[j] = c < C ? *reinterpret_cast<const u32x4 *>(row + 8 * c) : u32x4{};
+    const half8 h = __builtin_bit_cast(half8, v[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = __builtin_fmaxf(mx, __builtin_fabsf(static_cast<float>(h[e])));
+  }
+  mx = row_max(mx, wmax);
+  const int ex = row_exponent(mx);
+  const float f = __builtin_ldexpf(1.0f, ex);
+  if (threadIdx.x == 0) rscale[m] = __builtin_ldexpf(1.0f, -ex);
+  const int G = C >> 3;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    if (kPrepThreads * j >= C) break;                   // uniform: the butterfly needs every lane
+    const int c = threadIdx.x + kPrepThreads * j;
+    const half8 h = __builtin_bit_cast(half8, v[j]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum += static_cast<float>(h[e]) * f;
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    if (c >= C) continue;
+    *reinterpret_cast<u32x4 *>(xp + (size_t)m * K + 8 * c) = prep_x8_scaled(v[j], f);
+    if ((c & 7) == 0) write_gs_pieces<SD>(gs, gs_stride, m, c >> 3, G, sum);
+  }
+}
+
 // One workgroup per token row m. Pass 1 finds max |x| of the row; pass 2 writes
 // xp[m][k] (the row times 2^e, in operand order), gs[m][P g ..] (the pieces of the group
 // sums of the scaled row) and rscale[m] = 2^-e. One thread per 8 activations per step
@@ -99,7 +190,6 @@ template <int SD>
 __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(const _Float16 *x, int x_stride, int M, int K,
                                                                  _Float16 *xp, uint16_t *gs, int gs_stride,
                                                                  float *rscale) {
-  constexpr int P = kGsPieces<SD>;
   __shared__ float wmax[kPrepThreads / 64];
   const int m = blockIdx.x;
   const int C = K / 8;                                  // chunks per row (a multiple of 8)
@@ -110,18 +200,8 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(const _Float16 
 #pragma unroll
     for (int e = 0; e < 8; ++e) mx = __builtin_fmaxf(mx, __builtin_fabsf(static_cast<float>(h[e])));
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, d));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
-  __syncthreads();
-#pragma unroll
-  for (int w = 0; w < kPrepThreads / 64; ++w) mx = __builtin_fmaxf(mx, wmax[w]);
-  int ex = 0;
-  if (mx > 0.0f && mx <= 65504.0f) {
-    int k;
-    (void)__builtin_frexpf(mx, &k);                     // mx = f 2^k, f in [0.5, 1)
-    ex = 9 - k;                                         // mx 2^ex in [2^8, 2^9)
-  }
+  mx = row_max(mx, wmax);
+  const int ex = row_exponent(mx);
   const float f = __builtin_ldexpf(1.0f, ex);
   if (threadIdx.x == 0) rscale[m] = __builtin_ldexpf(1.0f, -ex);
   const int G = C >> 3;
@@ -139,27 +219,7 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(const _Float16 
     sum += __shfl_xor(sum, 4);
     if (!in) continue;
     *reinterpret_cast<u32x4 *>(xp + (size_t)m * K + 8 * c) = prep_x8_scaled(v, f);
-    if ((c & 7) == 0) {
-      const int g = c >> 3;
-      uint16_t *dst = gs + (size_t)m * gs_stride + P * g;
-      if constexpr (SD == 0) {
-        const _Float16 hi = static_cast<_Float16>(sum);
-        const _Float16 lo = static_cast<_Float16>(sum - static_cast<float>(hi));
-        dst[0] = __builtin_bit_cast(uint16_t, hi);
-        dst[1] = __builtin_bit_cast(uint16_t, lo);
-      } else {
-        const uint32_t hi = bf16_rne_bits(sum);
-        const float r1 = sum - __uint_as_float(hi << 16);         // exact
-        const uint32_t mid = bf16_rne_bits(r1);
-        const uint32_t lo = bf16_rne_bits(r1 - __uint_as_float(mid << 16));   // exact: 8 bits remain
-        dst[0] = (uint16_t)hi;
-        dst[1] = (uint16_t)mid;
-        dst[2] = (uint16_t)lo;
-        dst[3] = 0;
-      }
-      if (g == G - 1)   // the row's padding up to gs_stride is zero (no memset: this runs in graphs)
-        for (int k = P * G; k < gs_stride; ++k) gs[(size_t)m * gs_stride + k] = 0;
-    }
+    if ((c & 7) == 0) write_gs_pieces<SD>(gs, gs_stride, m, c >> 3, G, sum);
   }
 }
 
@@ -570,8 +630,15 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
     uint16_t *gs = reinterpret_cast<uint16_t *>(static_cast<char *>(ws) + xp_bytes);
     float *rscale = reinterpret_cast<float *>(static_cast<char *>(ws) + xp_bytes +
                                               ((size_t)M * gs_stride_of(G, 1) * 2 + 255) / 256 * 256);
-    if (sd == RLQ_BF16) gemm_prep_kernel<1><<<M, kPrepThreads, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale);
-    else gemm_prep_kernel<0><<<M, kPrepThreads, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale);
+    const int cpt = (K / 8 + kPrepThreads - 1) / kPrepThreads;   // chunks of the row per thread
+#define RLQ_PREP(KERNEL, ...)                                                                                          \
+  (sd == RLQ_BF16 ? KERNEL<1, ##__VA_ARGS__><<<M, kPrepThreads, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale) \
+                  : KERNEL<0, ##__VA_ARGS__><<<M, kPrepThreads, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale))
+    if (cpt <= 4) RLQ_PREP(gemm_prep1_kernel, 4);
+    else if (cpt <= 8) RLQ_PREP(gemm_prep1_kernel, 8);
+    else if (cpt <= 16) RLQ_PREP(gemm_prep1_kernel, 16);
+    else RLQ_PREP(gemm_prep_kernel);
+#undef RLQ_PREP
     RLQ_HIP(hipGetLastError());
     a.x = xp; a.x_stride = K; a.gs = gs; a.gs_stride = gs_stride; a.rscale = rscale;
   } else {

@@ -212,15 +212,19 @@ struct GemvArgs {
 // The workspace's first kGemvCountBytes hold the split counters (zero before the first
 // call; every call leaves them zero); the partials and the prefill kernel's data follow.
 constexpr size_t kGemvCountBytes = 4096;
-// S for a weight: 4 where the tiles are few (4 tiles <= 1280 workgroups) and each split
-// keeps at least 64 groups, else 1. The hand-over costs a few microseconds of latency at
+// S for a weight: 7 where the tiles are few (7 tiles <= 2240 workgroups) and each split
+// keeps at least 38 groups, else 1. The hand-over costs a few microseconds of latency at
 // the end (partials out, the count, partials back), which pays where K is long: measured
-// on the 27B down (K = 17408, N = 5120) at M = 1, 16.2 -> 13.3 us; on the 9B down
-// (K = 12288, N = 4096) a split in 2 lost (7.5 -> 8.9 us).
-constexpr int kSplit = 4;
+// on the 27B down (K = 17408, N = 5120) at M = 1, 16.2 -> 13.3 us with 4 splits; on the 9B
+// down (K = 12288, N = 4096) a split in 2 lost (7.5 -> 8.9 us). 7 rather than 4: at
+// M = 8 a split of the 27B down stages 40 groups of 8 rows (40 KB of LDS), so four
+// two-tile workgroups share a CU and its 1120 workgroups take 1.09 rounds of the chip,
+// against 1.25 for 640 workgroups of 68 groups (70 KB, two per CU): 27B layer at M = 8
+// 65.2 -> 62.2 us, M = 1 unchanged.
+constexpr int kSplit = 7;
 static int split_of(int K, int N) {
   const int G = K / kGroup, tiles = tiles_of(N);
-  return (long long)tiles * kSplit <= 1280 && G / kSplit >= 64 ? kSplit : 1;
+  return (long long)tiles * kSplit <= 2240 && G / kSplit >= 38 ? kSplit : 1;
 }
 static int gsplit_of(int K, int S) { return ((K / kGroup + S - 1) / S + 3) / 4 * 4; }
 
@@ -533,6 +537,16 @@ static int launch_gemv(int book, int sd, int accum, dim3 grid, int threads, size
 
 // book: kAffine (packed holds codes then scale/bias quads; sd their dtype) or a native
 // codebook (packed holds codes only; srow the row scales).
+// M > 1 with 8 groups per wave: two tiles per workgroup (each activation operand read once
+// for both) unless the grid is small (under 1024 tile splits) and the staged rows take at
+// most 48 KB, where one tile per workgroup puts twice the workgroups to work (three share
+// a CU): 9B layer at M = 5 37.6 -> 36.5 us; at the 27B qkv and o (80 KB of rows at M = 8)
+// the pairs stay faster. Both kernels give the same bits.
+static bool pair_tiles(int M, int K, int N) {
+  const int S = split_of(K, N);
+  return (long long)tiles_of(N) * S >= 1024 || (long long)M * (S == 1 ? K : gsplit_of(K, S) * kGroup) > 24576;
+}
+
 static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes, const void *sbq,
                     int sd, const float *srow, float *y, int y_stride, int accum, int *cnt, float *part,
                     size_t part_bytes, hipStream_t st) {
@@ -564,9 +578,10 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
                    : gpw == 12 ? launch_gemv<1, 12>(book, sd, accum, grid, threads, lds, st, a)
                    : gpw == 16 ? launch_gemv<1, 16>(book, sd, accum, grid, threads, lds, st, a)
                                : launch_gemv<1, 24>(book, sd, accum, grid, threads, lds, st, a);
-  else if (gpw == 8)   // two tiles per workgroup, activations staged in LDS
+  else if (gpw == 8 && pair_tiles(M, K, N))   // two tiles per workgroup, activations staged in LDS
     rc = launch_gemv<kGemvMaxM, 8, true>(book, sd, accum, dim3((tiles_of(N) + 1) / 2, S), threads, lds, st, a);
-  else rc = gpw == 12 ? launch_gemv<kGemvMaxM, 12>(book, sd, accum, grid, threads, lds, st, a)
+  else rc = gpw == 8 ? launch_gemv<kGemvMaxM, 8>(book, sd, accum, grid, threads, lds, st, a)
+            : gpw == 12 ? launch_gemv<kGemvMaxM, 12>(book, sd, accum, grid, threads, lds, st, a)
             : gpw == 16 ? launch_gemv<kGemvMaxM, 16>(book, sd, accum, grid, threads, lds, st, a)
                         : launch_gemv<kGemvMaxM, 24>(book, sd, accum, grid, threads, lds, st, a);
   if (rc) return rc;

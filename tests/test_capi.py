@@ -53,18 +53,18 @@ def test_abi_version_and_workspace_query():
     assert L.rlq_packed_affine_bytes(4096, 4096) == 256 * 16 * 2304
     assert L.rlq_packed_affine_bytes(64, 33) == 3 * 1 * 2304
     assert L.rlq_linear_workspace_bytes(256, 4096, 1024) > L.rlq_linear_workspace_bytes(64, 4096, 1024)
-    # the decode kernel splits K for few tiles and a long K (27B down: 4 splits): 4096 bytes
-    # of counters, then 4 x M x N partial floats; a workspace sized for M serves smaller M
-    assert L.rlq_linear_workspace_bytes(8, 17408, 5120) >= 4096 + 4 * 8 * 5120 * 4
-    assert L.rlq_linear_workspace_bytes(1, 17408, 5120) >= 4096 + 4 * 1 * 5120 * 4
+    # the decode kernel splits K for few tiles and a long K (27B down: 7 splits): 4096 bytes
+    # of counters, then 7 x M x N partial floats; a workspace sized for M serves smaller M
+    assert L.rlq_linear_workspace_bytes(8, 17408, 5120) >= 4096 + 7 * 8 * 5120 * 4
+    assert L.rlq_linear_workspace_bytes(1, 17408, 5120) >= 4096 + 7 * 1 * 5120 * 4
     assert L.rlq_linear_workspace_bytes(64, 17408, 5120) >= L.rlq_linear_workspace_bytes(8, 17408, 5120)
 
 
 def test_split_decode_without_workspace_is_an_error():
-    """A decode call on a weight whose K the kernel splits (here 4 ways: K = 17408, N = 640)
+    """A decode call on a weight whose K the kernel splits (here 7 ways: K = 17408, N = 640)
     needs the workspace for its partial sums and counters: without it the call fails before
     any launch (pointers are placeholders, never dereferenced)."""
-    with pytest.raises(lib.RlqError, match="splits K in 4"):
+    with pytest.raises(lib.RlqError, match="splits K in 7"):
         lib.call("rlq_linear_affine", 16, 17408, 1, 17408, 640, 16, 0, 16, 640, 0, None, 0, None)
 
 

@@ -141,7 +141,7 @@ def test_gemm_rows_do_not_depend_on_other_rows(gpu, K, N):
     np.testing.assert_array_equal(y_sub, y_all[50:120])
 
 
-@pytest.mark.parametrize("K,N", [(16384, 512), (16448, 40), (17408, 1000)])   # K split in 4; 257 groups; ragged N
+@pytest.mark.parametrize("K,N", [(17024, 512), (17472, 40), (17408, 1000)])   # K split in 7; 266 and 273 groups; ragged N
 def test_split_k_decode_between_other_calls(gpu, K, N):
     """Weights whose K the decode kernel splits across workgroups (few tiles, long K) keep
     their arrival counters in the workspace's first bytes and leave them zero: a split call,
@@ -276,7 +276,7 @@ def test_reference_correctness_cases(gpu, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 17408, 40), (5, 17408, 40), (1, 640, 48), (3, 2560, 33),
-                                   (1, 16448, 40), (8, 16448, 40)])   # K split in 4, the last split short
+                                   (1, 17472, 40), (8, 17472, 40)])   # K split in 7, the last split short
 def test_gemv_reads_nothing_past_the_weight(gpu, M, K, N):
     """A wave's last groups past K (K not a multiple of its group range) must read zeros,
     not whatever follows the packed weight in memory: the weight sits at the head of a

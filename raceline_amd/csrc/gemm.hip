@@ -20,7 +20,10 @@
 // prescale, then the operand order (x0, x4, x1/16, x5/16, ...) of the five-op code
 // conversion), and the outputs are scaled back at the store. The bias term
 // sum_g b[n][g] gsum[m][g] is one more MFMA product at the end, over K' = 2G, with the
-// group sums split into fp16 hi + lo (exact to 2^-22) and b as the other operand.
+// group sums split into fp16 hi + lo (exact to 2^-22) and b as the other operand; the
+// group sums of the tile's rows go through the LDS once per workgroup for all its waves.
+// The K loop runs three group pairs per iteration, one per LDS stage, so every LDS read has
+// a compile-time stage offset; workgroups are ordered in groups of 4 token blocks per XCD.
 // Native books: activations are used as they are, codes decode in element order, and the
 // products chain in the MFMA over all of K with the row scale applied at the end.
 // A row's result depends only on its own activations (MFMA rows are independent).
@@ -248,8 +251,8 @@ __device__ __forceinline__ void issue_stage(const StageSrc &s, unsigned char *ld
   if (128 * (p + 1) <= s.K) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, a_part(stage) + (4 * s.wave + i) * 1024), 16, s.a_off[i],
-                                               256 * p, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rx, lds_at(lds, a_part(stage) + (4 * s.wave + i) * 1024), 16,
+                                               s.a_off[i], 256 * p, 0, 0);
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -502,10 +505,8 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
 #pragma unroll
       for (int u = 0; u < kBiasChunk; ++u) {
         const int q = SD == 0 ? 2 * (st0 + u) + h : st0 + u;   // quad of groups 4q .. 4q+3
-        v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rs, u < cs && q < G4 ? (uint32_t)tt * G4 * 256u + (uint32_t)q * 256u + 16u * cr
-                                                                  : kFarOffset,
-                                             0, 0));
+        const uint32_t off = u < cs && q < G4 ? (uint32_t)tt * G4 * 256u + (uint32_t)q * 256u + 16u * cr : kFarOffset;
+        v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0): this wave's LDS reads are done
       asm volatile("s_barrier" ::: "memory");               // and every wave's
@@ -610,8 +611,9 @@ static int launch_gemm4_inst(int accum, dim3 grid, size_t lds, hipStream_t st, c
   return 0;
 }
 
-int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes, const void *sbq, int sd,
-              const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes, hipStream_t st) {
+int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes, const void *sbq,
+              int sd, const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes,
+              hipStream_t st) {
   const int G = K / kGroup;
   const size_t need = gemm4_workspace(book, M, K, N);
   RLQ_REQUIRE(ws_bytes >= need, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);

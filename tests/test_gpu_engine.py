@@ -180,6 +180,75 @@ def test_moe_mlp(gpu, tmp_path, book):
         assert hits.value == 0 and loads.value == 0
 
 
+def _check_layer(got, ref, what):
+    """A layer's contribution through fp16 activations, against the fp64 reference that
+    rounds the same activations: where the kernel's fp32 value and the fp64 one fall on
+    either side of a rounding point, the two activations are one half ulp apart, which
+    moves every output of that token's row. So the bulk is held tight (rms error <= 2e-4
+    of the rms) and isolated rows may carry such a step (max <= 3e-3 of the rms); measured
+    at these sizes: bulk <= 9.3e-5, single-activation rows up to 1.8e-3, other rows exact
+    or near 3e-5."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert np.isfinite(got).all(), f"{what}: non-finite values"
+    rms = float(np.sqrt(np.mean(ref ** 2)))
+    err = got - ref
+    bulk = float(np.sqrt(np.mean(err ** 2))) / rms
+    worst = float(np.abs(err).max()) / rms
+    assert bulk <= 2e-4 and worst <= 3e-3, f"{what}: rms err/rms = {bulk:.3e}, max err/rms = {worst:.3e}"
+
+
+@pytest.mark.parametrize("book", [None, "int15"])
+@pytest.mark.parametrize("hidden,inter,vocab", [(320, 768, 700), (512, 256, 1300)])
+def test_dense_layer_and_head_other_sizes(gpu, tmp_path, book, hidden, inter, vocab):
+    """Model sizes the other tests do not use: a hidden size of 5 groups (320) or 8 (512),
+    intermediate sizes of 768 and 256, and vocabularies that are not a multiple of the
+    256-row block (the head's padding rows). rl_mlp at decode and prefill row counts and
+    rl_head against the fp64 reference: the head within 1e-3 (one product), the MLP by
+    _check_layer (its contribution passes through fp16 activations)."""
+    m = MF.write_dense_model(str(tmp_path / "m.rlm"), seed=hidden + inter, native_book=book, hidden=hidden,
+                             intermediate=inter, vocab=vocab, layers=1)
+    with Engine(m.path, max_chunk=64) as e:
+        assert e.vocab == vocab and e.hidden_size == hidden
+        for T in (1, 7, 33):
+            h0 = np.random.default_rng(T + hidden).standard_normal((T, hidden)).astype(np.float32)
+            h = to_dev(h0, gpu)
+            e.mlp(0, h)
+            _sync()
+            ref = _mlp_ref(m, 0, h0)
+            _check_layer(h.cpu().numpy().astype(np.float64) - h0, ref - h0, f"dense MLP T={T} H={hidden} I={inter} "
+                         f"book={book}")
+        h0 = np.random.default_rng(vocab).standard_normal((3, hidden)).astype(np.float32)
+        logits = e.head(to_dev(h0, gpu))
+        _sync()
+        w = m.floats["final_norm"]
+        c = _col_scale(m, "lm_head")
+        if c is not None:
+            w = (w * c).astype(np.float32)
+        ref = MF.linear_f64(m, "lm_head", OE.rms_norm_f16(h0, w, m.cfg["rms_norm_eps"]))
+        got = logits.cpu().numpy()
+        O.check_close(got[:, :vocab], ref, TOL, f"head vocab={vocab} H={hidden} book={book}")
+        assert (got[:, vocab:] == 0).all()                     # padding rows of the head
+
+
+@pytest.mark.parametrize("book", [None, "fp4"])
+def test_moe_layer_other_sizes(gpu, tmp_path, book):
+    """A mixture of experts of other sizes (H = 512, 32 experts + shared, top-3, I = 384; the
+    reader takes expert counts that are multiples of 32, as src/model_file.mm:75 does)
+    through rl_mlp at one token, a few, and a batch on the staged kernels, checked by
+    _check_layer."""
+    m = MF.write_moe_model(str(tmp_path / "moe.rlm"), seed=21, native_book=book, hidden=512, experts=32, topk=3,
+                           moe_inter=384)
+    with Engine(m.path, max_chunk=64) as e:
+        for T in (1, 5, 40):
+            h0 = np.random.default_rng(300 + T).standard_normal((T, 512)).astype(np.float32)
+            h = to_dev(h0, gpu)
+            e.mlp(0, h)
+            _sync()
+            ref = _moe_ref(m, 0, h0)
+            _check_layer(h.cpu().numpy().astype(np.float64) - h0, ref - h0, f"MoE T={T} book={book}")
+
+
 @pytest.mark.parametrize("book", BOOKS)
 def test_head_draft_vocab_and_top_k(gpu, tmp_path, book):
     import torch

@@ -2,7 +2,8 @@
 
 The other files pin fixed cases (the BASELINE configs, the reference's own cases, edge
 shapes); these draw ragged M, K and N at random (fixed seeds, so a failure names its shape
-and reproduces), with both scale types, the three native codebooks and random MoE layers.
+and reproduces), with both scale types, the three native codebooks, decode sizes long
+enough for the K split, and random MoE layers.
 Same bars as the other files: max|y - ref| / rms(ref) <= 1e-3 and the reference's own
 criterion (tests/test_linear.mm:178), both via oracle.check_close.
 """
@@ -44,6 +45,24 @@ def test_affine_random_shapes(gpu, M, K, N):
     y = ops.linear(to_dev(x, gpu), upload(q, s, b, sd, gpu))
     _sync()
     O.check_close(y.cpu().numpy(), O.linear_affine_f64(x, q, s, b, sd), TOL, f"affine {sd} M={M} K={K} N={N}")
+
+
+def _split_shapes(seed, n):
+    """Decode sizes whose K the kernel splits across workgroups (K >= 17024, few tiles)."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.choice([1, 2, 5, 8])), 64 * int(rng.integers(266, 385)), int(rng.integers(1, 3000)))
+            for _ in range(n)]
+
+
+@pytest.mark.parametrize("M,K,N", _split_shapes(2029, 5))
+def test_affine_random_split_decode(gpu, M, K, N):
+    from raceline_amd import ops
+
+    q, s, b = make_layer(M + K + N, N, K, "f16")
+    x = make_x(K + N, M, K)
+    y = ops.linear(to_dev(x, gpu), upload(q, s, b, "f16", gpu))
+    _sync()
+    O.check_close(y.cpu().numpy(), O.linear_affine_f64(x, q, s, b, "f16"), TOL, f"split decode M={M} K={K} N={N}")
 
 
 @pytest.mark.parametrize("M,K,N", _shapes(2027, 12, 72))

@@ -151,12 +151,13 @@ __device__ __forceinline__ void issue_tile_loads(const WaveTile &w, int lane, u3
   }
 }
 
-// Activations -> operand order: the affine path's permuted order (prep_x8); native books
-// take the natural order.
+// Activations -> operand order: the permuted order of prep_x8 for the affine and integer
+// books (whose code conversions, nib8_to_half8_sub and native8_operand, give that order),
+// the element order for fp4.
 template <int BOOK>
 __device__ __forceinline__ u32x4 prep_act(u32x4 v) {
-  if constexpr (BOOK == kAffine) return prep_x8(v);
-  else return v;
+  if constexpr (BOOK == kFp4) return v;
+  else return prep_x8(v);
 }
 
 // One group of a native-book tile: the products chain straight into the accumulator (no
@@ -167,7 +168,8 @@ __device__ __forceinline__ void native_step(f32x4 &acc, f32x4 &asum, const half8
   const half8 ones = __builtin_bit_cast(half8, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq[jg >> 1][2 * (jg & 1) + s]), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_operand<BOOK>(wq[jg >> 1][2 * (jg & 1) + s]), acc, 0,
+                                                 0, 0);
     if constexpr (BOOK == kInt16) asum = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, asum, 0, 0, 0);
   }
 }
@@ -302,9 +304,9 @@ __device__ __forceinline__ void tile_dot_rows2(const WaveTile &w0, const WaveTil
     } else {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq0[jg >> 1][2 * (jg & 1) + s]),
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_operand<BOOK>(wq0[jg >> 1][2 * (jg & 1) + s]),
                                                       acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq1[jg >> 1][2 * (jg & 1) + s]),
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_operand<BOOK>(wq1[jg >> 1][2 * (jg & 1) + s]),
                                                       acc1, 0, 0, 0);
         if constexpr (BOOK == kInt16) asum = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, asum, 0, 0, 0);
       }
@@ -389,9 +391,9 @@ __device__ __forceinline__ void tile_dot_rows2_staged(const WaveTile &w0, const 
     } else {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq0[jg >> 1][2 * (jg & 1) + s]),
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_operand<BOOK>(wq0[jg >> 1][2 * (jg & 1) + s]),
                                                       acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_to_half8<BOOK>(wq1[jg >> 1][2 * (jg & 1) + s]),
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], native8_operand<BOOK>(wq1[jg >> 1][2 * (jg & 1) + s]),
                                                       acc1, 0, 0, 0);
         if constexpr (BOOK == kInt16) asum = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], ones, asum, 0, 0, 0);
       }
@@ -516,7 +518,7 @@ __device__ __forceinline__ void tile_dot_lds(const u32x4 (&wq)[GPW / 2], const u
 #pragma unroll
         for (int s = 0; s < 2; ++s)
           acc[jg / per] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              af[s], native8_to_half8<BOOK>(wq[jg >> 1][2 * (jg & 1) + s]), acc[jg / per], 0, 0, 0);
+              af[s], native8_operand<BOOK>(wq[jg >> 1][2 * (jg & 1) + s]), acc[jg / per], 0, 0, 0);
       }
       asm volatile("" : "+v"(acc[jg / per]));
     }

@@ -96,27 +96,50 @@ __device__ __forceinline__ half8 nib8_to_half8(uint32_t u) {
 // kernels/linear.metal:128-129,171-172 do); kFp4: e2m1, sign in bit 3.
 enum Book { kAffine = 0, kInt15 = 1, kInt16 = 2, kFp4 = 3 };
 
-// Eight native codes -> their codebook values as fp16, in element order.
+// Eight native codes -> their codebook values as fp16, in element order. kFp4: the
+// hardware's e2m1 -> fp16 conversion, two codes (one byte, low nibble first) per
+// instruction; with scale 1 every value is exact: 0, 0.5, 1, 1.5, 2, 3, 4, 6, signed by
+// bit 3 (the same bits as a table lookup of the codebook).
 template <int BOOK>
 __device__ __forceinline__ half8 native8_to_half8(uint32_t u) {
   if constexpr (BOOK == kFp4) {
-    // magnitude index 0..7 -> high byte of its fp16 value through a byte table (v_perm
-    // picks from 8 bytes): 0, 0.5, 1, 1.5, 2, 3, 4, 6 = 0x00, 0x38, 0x3C, 0x3E, 0x40, 0x42, 0x44, 0x46
-    constexpr uint32_t kLutLo = 0x3E3C3800u, kLutHi = 0x46444240u;
-    const uint32_t mlo = u & 0x07070707u, mhi = (u >> 4) & 0x07070707u;
-    const uint32_t slo = u & 0x08080808u, shi = (u >> 4) & 0x08080808u;
     u32x4 d;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t pick = 0x040C000Cu + 0x01000100u * i;            // bytes [0, m(2i), 0, m(2i+1)]
-      const uint32_t sel = __builtin_amdgcn_perm(mhi, mlo, pick) | 0x000C000Cu;
-      const uint32_t mag = __builtin_amdgcn_perm(kLutHi, kLutLo, sel);
-      const uint32_t sgn = __builtin_amdgcn_perm(shi, slo, pick) << 4;  // bit 3 of each code -> bit 15
-      d[i] = mag | sgn;
-    }
+    d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1.0f, 0));
+    d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1.0f, 1));
+    d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1.0f, 2));
+    d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1.0f, 3));
     return __builtin_bit_cast(half8, d);
   } else {
     return nib8_to_half8<8>(u ^ 0x88888888u);   // (q ^ 8) - 8: the signed value
+  }
+}
+
+// Eight native codes -> matrix-core operands in the order the tile kernels feed them:
+// kFp4 in element order (native8_to_half8); kInt15 and kInt16 in the permuted order
+// (q0, q4, q1, q5, q2, q6, q3, q7) of the affine path, which needs no byte permutes: with
+// q' = q ^ 8, a mask puts codes 0 and 4 (2 and 6 after a shift by 8) in the mantissas of
+// two normal fp16 numbers over the exponent pattern 0x6400, as 1024 + q', and codes 1 and 5
+// (3 and 7) as 1024 + 16 q'; one packed add, or fused multiply-add, per pair then gives
+// q' - 8, the signed value, exactly: (1024 + q') - 1032 and (1024 + 16 q') / 16 - 72. Ten
+// operations for eight codes, against sixteen in element order.
+template <int BOOK>
+__device__ __forceinline__ half8 native8_operand(uint32_t u) {
+  if constexpr (BOOK == kFp4) {
+    return native8_to_half8<kFp4>(u);
+  } else {
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+    const uint32_t v = u ^ 0x88888888u, t = v >> 8;
+    const half2v off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const half2v sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f}, off16 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    auto lo = [&](uint32_t w) {
+      return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, (w & 0x000F000Fu) | 0x64006400u) + off);
+    };
+    auto hi = [&](uint32_t w) {
+      return __builtin_bit_cast(uint32_t,
+                                __builtin_bit_cast(half2v, (w & 0x00F000F0u) | 0x64006400u) * sixteenth + off16);
+    };
+    const u32x4 d = {lo(v), hi(v), lo(t), hi(t)};
+    return __builtin_bit_cast(half8, d);
   }
 }
 

@@ -153,19 +153,23 @@ def test_native_layer_matches_oracle(gpu, book, T, E, topk, H, I):
 
 
 @pytest.mark.parametrize("book", ["int15", "fp4"])
-@pytest.mark.parametrize("H,I", [(512, 256), (4096, 64)])
-def test_native_gate_up_fused_equals_two_launches(gpu, book, H, I):
+@pytest.mark.parametrize("H,I,T,bad", [(512, 256, 9, False), (4096, 64, 9, False), (2048, 128, 12, False),
+                                       (512, 256, 3, False), (1024, 192, 10, True), (512, 128, 2, True)])
+def test_native_gate_up_fused_equals_two_launches(gpu, book, H, I, T, bad):
     """rlq_moe_gate_up_native gives the bits of the gate/up product followed by the SwiGLU,
-    with and without a column scale."""
+    with and without a column scale, at 8 and 16 groups per wave and ragged I. bad: two
+    experts' slots point outside the table (zero rows before the SwiGLU)."""
     import torch
 
     from raceline_amd import ops
 
-    rng = np.random.default_rng(H + I)
-    E, T, topk = 16, 9, 4
+    rng = np.random.default_rng(H + I + T)
+    E, topk = 16, 4
     codes, s_row = make_stack(rng, E + 1, 2 * I, H, book)
     slots = shuffled_slots(rng, E, 1)
     c2, s2 = place(codes, s_row, slots, 2 * I, E + 2)
+    if bad:
+        slots[3], slots[E] = -1, E + 2
     st = upload_stack(c2, s2, 2 * I, book, gpu)
     r = ops.moe_route(to_dev(rng.standard_normal((T, E + 1), dtype=np.float32), gpu), E, topk)
     x = to_dev(rng.standard_normal((T, H)).astype(np.float16), gpu)

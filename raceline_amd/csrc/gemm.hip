@@ -46,6 +46,7 @@ constexpr int kStageBytes = kABytes + kBBytes + kSBytes;
 constexpr int kStages = 3;                  // loads run two group pairs ahead of the MFMAs
 constexpr int kGroupM = 4;                  // token blocks per group of the workgroup order
 constexpr int kBiasChunk = 32;              // bias product: steps of group-sum pieces staged at a time
+constexpr int kMaxGemmSplit = 2;            // workgroups per output tile when K is split
 // LDS by part, then stage: the three activation tiles, the three code parts, the three
 // scale parts, so that with the stage known at compile time every read of a stage is a
 // lane's base address plus an immediate offset
@@ -310,14 +311,14 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   const int G = a.K / kGroup, G4 = quads_of(a.K), GP = 2 * G4;
   const int NP = (G + 1) / 2;                        // group pairs with real groups
   const int T = tiles_of(a.N);
-  // Split K (gridDim.y == 2): the first half of the pairs adds the bias term and writes y
-  // (accumulating when asked); the second writes its partial products to y_part, which a
-  // second kernel adds to y, so the two halves always meet in the same order.
-  const int split = blockIdx.y;
-  const int pb = split == 0 ? 0 : a.np_first;
-  const int NPs = split == 0 ? a.np_first : NP - a.np_first;
-  float *const yout = split == 0 ? a.y : a.y_part;
-  const int ystride = split == 0 ? a.y_stride : a.y_part_stride;
+  // Split K (S = gridDim.y > 1, see gemm_split_of): split s takes group pairs
+  // [s P, s P + P) (P = np_split, the last split the rest) and its share of the bias steps;
+  // split 0 writes y (adding to it when asked), split s > 0 its partial products to
+  // y_part[s - 1]; the tile's last split to arrive adds them in split order (see the end of
+  // the kernel).
+  const int split = blockIdx.y, S = gridDim.y;
+  const int pb = split * a.np_split;
+  const int NPs = min(NP, pb + a.np_split) - pb;
   const bool acc_here = ACC && split == 0;
 
   // Workgroups are numbered round-robin over the 8 XCDs; give each XCD a contiguous
@@ -482,9 +483,11 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
     }
   }
 
-  if (BOOK == kAffine && split == 0) {
+  if (BOOK == kAffine) {
     // acc += sum_g b[n][g] * gsum[m][g]: an MFMA product over K' = P G, each group sum as P
-    // pieces (gemm_prep_kernel). Step st covers k' = 16 st .. +15; lane half h holds k'
+    // pieces (gemm_prep_kernel); a split K shares its steps out evenly over the splits (each
+    // split adds its share; any division covers every step once). Step st covers
+    // k' = 16 st .. +15; lane half h holds k'
     // 16 st + 8 h .. +7: for fp16 biases (P = 2) the (hi, lo) of groups 8 st + 4 h .. +3, so
     // b of those groups, each twice; for bf16 biases (P = 4) the pieces of groups
     // 4 st + 2 h and + 1, so b of those two, four times each. Every wave needs the pieces of
@@ -498,8 +501,9 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sb + (size_t)min(tn, T) * G4 * 16, (uint32_t)tv * G4 * 256u);
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.gs, (uint32_t)((size_t)a.M * a.gs_stride * 2));
     const int steps = a.gs_stride / 16;
-    for (int st0 = 0; st0 < steps; st0 += kBiasChunk) {
-      const int cs = min(kBiasChunk, steps - st0);
+    const int st_lo = split * steps / S, st_hi = (split + 1) * steps / S;
+    for (int st0 = st_lo; st0 < st_hi; st0 += kBiasChunk) {
+      const int cs = min(kBiasChunk, st_hi - st0);
       const int rowb = 32 * cs + 16;                       // LDS bytes per row
       u32x4 v[kBiasChunk];
 #pragma unroll
@@ -548,36 +552,115 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
     }
   }
 
-  // D of a 32x32 tile: lane l holds column l%32, rows 8 (v/4) + 4 (l/32) + v%4
+  // D of a 32x32 tile: lane l holds column l%32, rows 8 (v/4) + 4 (l/32) + v%4. acc becomes
+  // this split's values (split 0's with y added when asked).
   const int n = n0 + 32 * wave + c32;
-  if (n >= a.N) return;
-  const float rs_n = BOOK == kAffine || !a.srow ? 1.0f : a.srow[n];   // no row scales: the raw product
+  const bool col = n < a.N;
+  const float rs_n = BOOK == kAffine || !a.srow || !col ? 1.0f : a.srow[n];   // no row scales: the raw product
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-      if (m < a.M) {
+      if (col && m < a.M) {
         float val = acc[mt][v];
         if constexpr (BOOK == kAffine) val *= a.rscale[m];   // undoes the prep's 2^e, exactly
         if constexpr (BOOK == kInt16) {
           if (split == 0) val = __builtin_fmaf(0.5f, a.asum[m], val);
         }
         if constexpr (BOOK != kAffine) val *= rs_n;
-        float *dst = yout + (size_t)m * ystride + n;
-        *dst = acc_here ? *dst + val : val;
+        if (acc_here) val = a.y[(size_t)m * a.y_stride + n] + val;
+        acc[mt][v] = val;
       }
+    }
+  }
+  if (S == 1) {
+    if (!col) return;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (m < a.M) a.y[(size_t)m * a.y_stride + n] = acc[mt][v];
+      }
+    return;
+  }
+
+  // Split K. Every split stores its values (split 0 in y, split s in y_part[s - 1]) with
+  // agent-scope atomic stores, the coherent accesses every XCD sees, waits for them, and the
+  // workgroup counts its arrival on the tile's counter. The split whose arrival is the
+  // S-th adds the S values in split order (its own from registers, the others by
+  // agent-scope atomic loads), writes y and sets the counter back to zero. No workgroup
+  // waits for another, so nothing assumes the splits run at the same time.
+  float *const mine = split == 0 ? a.y : a.y_part + (size_t)(split - 1) * a.M * a.N;
+  const int mstride = split == 0 ? a.y_stride : a.N;
+  if (col) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (m < a.M)
+          __hip_atomic_store(mine + (size_t)m * mstride + n, acc[mt][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+  }
+  __builtin_amdgcn_s_waitcnt(0);                     // this wave's values are stored
+  __syncthreads();                                   // and every wave's
+  int *const arrival = reinterpret_cast<int *>(lds);   // the ring and the bias pieces are done with
+  const int tile = mb * ((a.N + kGN - 1) / kGN) + nb;
+  if (tid == 0) arrival[0] = __hip_atomic_fetch_add(a.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (arrival[0] != S - 1) return;                   // uniform: the tile's last split goes on
+  if (tid == 0) __hip_atomic_store(a.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!col) return;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    // every value of this token tile is requested before the first is added
+    float p[kMaxGemmSplit][16];
+#pragma unroll
+    for (int s = 0; s < kMaxGemmSplit; ++s) {
+      if (s >= S || s == split) continue;            // uniform
+      const float *src = s == 0 ? a.y : a.y_part + (size_t)(s - 1) * a.M * a.N;
+      const int sstride = s == 0 ? a.y_stride : a.N;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = min(m0 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3), a.M - 1);
+        p[s][v] = __hip_atomic_load(src + (size_t)m * sstride + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+      float sum = split == 0 ? acc[mt][v] : p[0][v];
+#pragma unroll
+      for (int s = 1; s < kMaxGemmSplit; ++s)
+        if (s < S) sum += s == split ? acc[mt][v] : p[s][v];
+      if (m < a.M) a.y[(size_t)m * a.y_stride + n] = sum;
     }
   }
 }
 
 // ------------------------------------------------------------------ host
 
-// K is split in two when the reduction is long against the output width (K >= 2N, and
-// at least 32 group pairs): the down projections, whose few output tiles would otherwise
-// leave most of the chip idle in the last round of workgroups. The choice depends on the
-// shape only, never on M, so a token's result is the same whatever the batch.
-static bool split_k(int K, int N) { return K >= 2 * N && (K / kGroup + 1) / 2 >= 32; }
+// K is split over S = 2 workgroups per output tile where that fills the rounds of the chip
+// far better and the reduction is long: the workgroup takes about the same time per group
+// pair whatever the shape (one 8-wave workgroup per CU), so a launch takes ceil(tiles S /
+// 256) rounds of 1/S of a tile's time, plus the partials' hand-over (each split stores its
+// 128 x 256 floats, the last one loads the others: measured about 20 us per launch of the
+// 27B o or down projection at M = 2048). For a 2048-token chunk (16 token blocks) the 27B
+// down projection (20 feature blocks, K = 17408) has 320 tiles, 1.25 rounds unsplit, 2.5
+// split (497 -> 435 us with the prep pass); the o projection (the same tiles at K = 5120)
+// gains less than the hand-over costs (180 -> 183 us), and 4 splits of either were slower
+// still (198 and 440 us). So S = 2 for weights of at most 32 feature blocks whose rounds at
+// 16 token blocks are at least 1.25 times fuller split, and whose K holds 64 group pairs or
+// more. The choice depends on the weight's shape only, never on M, so a token's result is
+// the same whatever the batch.
+static double round_fill(int tiles) { return tiles / (256.0 * ((tiles + 255) / 256)); }
+static int gemm_split_of(int K, int N) {
+  const int nblocks = (N + kGN - 1) / kGN, NP = (K / kGroup + 1) / 2;
+  if (nblocks > 32 || NP < 64) return 1;
+  return round_fill(32 * nblocks) >= 1.25 * round_fill(16 * nblocks) ? kMaxGemmSplit : 1;
+}
 
 static size_t books_workspace(int book, int M, int K) {
   const int G = K / kGroup;
@@ -588,14 +671,13 @@ static size_t books_workspace(int book, int M, int K) {
   return 0;
 }
 
-size_t gemm4_workspace(int book, int M, int K, int N) {
-  return books_workspace(book, M, K) + (split_k(K, N) ? (size_t)M * N * sizeof(float) : 0);
-}
+// Rows of one launch of a split weight: as many whole token blocks as have counters.
+static int split_chunk_rows(int N) { return kGemmMaxCounters / ((N + kGN - 1) / kGN) * kGM; }
 
-// y[m][n] += part[m][n]: the second half of a split K, added in a fixed order.
-__global__ void split_add_kernel(float *y, int y_stride, const float *part, int part_stride, int M, int N) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
-  if (n < N && m < M) y[(size_t)m * y_stride + n] += part[(size_t)m * part_stride + n];
+size_t gemm4_workspace(int book, int M, int K, int N) {
+  const int S = gemm_split_of(K, N);
+  const size_t rows = S > 1 ? (size_t)std::min(M, split_chunk_rows(N)) : 0;
+  return books_workspace(book, M, K) + (size_t)(S - 1) * rows * N * sizeof(float);
 }
 
 template <int BOOK, int SD>
@@ -612,7 +694,7 @@ static int launch_gemm4_inst(int accum, dim3 grid, size_t lds, hipStream_t st, c
 }
 
 int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes, const void *sbq,
-              int sd, const float *srow, float *y, int y_stride, int accum, void *ws, size_t ws_bytes,
+              int sd, const float *srow, float *y, int y_stride, int accum, int *cnt, void *ws, size_t ws_bytes,
               hipStream_t st) {
   const int G = K / kGroup;
   const size_t need = gemm4_workspace(book, M, K, N);
@@ -654,28 +736,35 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
       a.asum = asum;
     }
   }
-  const bool split = split_k(K, N);
-  a.np_first = split ? (G + 1) / 2 / 2 : (G + 1) / 2;
-  if (split) {
-    a.y_part = reinterpret_cast<float *>(static_cast<char *>(ws) + books_workspace(book, M, K));
-    a.y_part_stride = N;
-  }
-  const int mblocks = (M + kGM - 1) / kGM, nblocks = (N + kGN - 1) / kGN;
-  const dim3 grid(mblocks * nblocks, split ? 2 : 1);
+  const int S = gemm_split_of(K, N);
+  RLQ_REQUIRE(S == 1 || cnt, "prefill kernel: this weight splits K in %d, which needs the workspace's counters", S);
+  a.np_split = ((G + 1) / 2 + S - 1) / S;
+  a.cnt = cnt;
+  if (S > 1) a.y_part = reinterpret_cast<float *>(static_cast<char *>(ws) + books_workspace(book, M, K));
+  const int nblocks = (N + kGN - 1) / kGN;
   const size_t lds = (size_t)kStages * kStageBytes;
-  int rc;
-  switch (book) {
-    case kInt15: rc = launch_gemm4_inst<kInt15, 0>(accum, grid, lds, st, a); break;
-    case kInt16: rc = launch_gemm4_inst<kInt16, 0>(accum, grid, lds, st, a); break;
-    case kFp4: rc = launch_gemm4_inst<kFp4, 0>(accum, grid, lds, st, a); break;
-    default:
-      rc = sd == RLQ_BF16 ? launch_gemm4_inst<kAffine, 1>(accum, grid, lds, st, a)
-                          : launch_gemm4_inst<kAffine, 0>(accum, grid, lds, st, a);
-  }
-  if (rc) return rc;
-  RLQ_HIP(hipGetLastError());
-  if (split) {
-    split_add_kernel<<<dim3((N + 255) / 256, M), 256, 0, st>>>(y, y_stride, a.y_part, a.y_part_stride, M, N);
+  // a split weight launches in chunks of rows whose tiles have counters; the rows are
+  // independent, so chunking changes no result
+  const int chunk = S > 1 ? split_chunk_rows(N) : M;
+  for (int r0 = 0; r0 < M; r0 += chunk) {
+    GemmArgs c = a;
+    c.M = std::min(chunk, M - r0);
+    c.x = a.x + (size_t)r0 * a.x_stride;
+    c.y = a.y + (size_t)r0 * a.y_stride;
+    if (a.gs) c.gs = a.gs + (size_t)r0 * a.gs_stride;
+    if (a.rscale) c.rscale = a.rscale + r0;
+    if (a.asum) c.asum = a.asum + r0;
+    const dim3 grid((c.M + kGM - 1) / kGM * nblocks, S);
+    int rc;
+    switch (book) {
+      case kInt15: rc = launch_gemm4_inst<kInt15, 0>(accum, grid, lds, st, c); break;
+      case kInt16: rc = launch_gemm4_inst<kInt16, 0>(accum, grid, lds, st, c); break;
+      case kFp4: rc = launch_gemm4_inst<kFp4, 0>(accum, grid, lds, st, c); break;
+      default:
+        rc = sd == RLQ_BF16 ? launch_gemm4_inst<kAffine, 1>(accum, grid, lds, st, c)
+                            : launch_gemm4_inst<kAffine, 0>(accum, grid, lds, st, c);
+    }
+    if (rc) return rc;
     RLQ_HIP(hipGetLastError());
   }
   return 0;

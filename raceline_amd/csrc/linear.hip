@@ -212,6 +212,7 @@ struct GemvArgs {
 // The workspace's first kGemvCountBytes hold the split counters (zero before the first
 // call; every call leaves them zero); the partials and the prefill kernel's data follow.
 constexpr size_t kGemvCountBytes = 4096;
+static_assert(kGemvCountBytes == kGemmMaxCounters * sizeof(int), "the prefill split shares the counters");
 // S for a weight: 7 where the tiles are few (7 tiles <= 2240 workgroups) and each split
 // keeps at least 38 groups, else 1. The hand-over costs a few microseconds of latency at
 // the end (partials out, the count, partials back), which pays where K is long: measured
@@ -602,7 +603,7 @@ int linear_packed(int kernel, int book, const _Float16 *x, int x_stride, int M, 
   if (gemv)
     return run_gemv(book, x, x_stride, M, K, N, codes, sbq, sd, srow, y, y_stride, accum, cnt,
                     static_cast<float *>(rest), rest_bytes, st);
-  return run_gemm4(book, x, x_stride, M, K, N, codes, sbq, sd, srow, y, y_stride, accum, rest, rest_bytes, st);
+  return run_gemm4(book, x, x_stride, M, K, N, codes, sbq, sd, srow, y, y_stride, accum, cnt, rest, rest_bytes, st);
 }
 
 // ================================================================== group sums

@@ -90,7 +90,7 @@ GEMM_CASES = [(9, 512, 96), (16, 1024, 300), (32, 2048, 1024), (33, 256, 64), (1
               (512, 2048, 1024), (70, 9216, 2560), (256, 1024, 300), (40, 2560, 1000),
               # an odd number of groups (the last pair half empty), a single group, ragged M and N
               (129, 320, 17), (64, 64, 48), (200, 576, 272), (300, 192, 513),
-              # K split in two halves (K >= 2N, >= 32 group pairs), with an odd number of groups
+              # a long K with an odd number of groups
               (100, 4160, 1000)]
 
 
@@ -139,6 +139,61 @@ def test_gemm_rows_do_not_depend_on_other_rows(gpu, K, N):
     y_all = _run(gpu, x, wt, kernel=2)
     y_sub = _run(gpu, x[50:120], wt, kernel=2)
     np.testing.assert_array_equal(y_sub, y_all[50:120])
+
+
+# Weights whose K the prefill kernel splits over 2 workgroups per output tile (from the
+# weight's shape: at most 32 feature blocks, 64 group pairs or more, rounds at 16 token
+# blocks 1.25 times fuller split): an odd number of groups (K = 8256: splits of 33 and 32
+# group pairs, the last pair half empty), bf16 biases, ragged M and N, the 27B down shape.
+SPLIT_GEMM_CASES = [(150, 8192, 1024, "f16"), (300, 8256, 1000, "f16"), (257, 9216, 600, "bf16"),
+                    (130, 17408, 5120, "f16")]
+
+
+@pytest.mark.parametrize("M,K,N,sd", SPLIT_GEMM_CASES)
+def test_gemm_split_k(gpu, M, K, N, sd):
+    """The last split to arrive adds the partials in split order: the result matches the
+    oracle, with ACCUM too, and a repeat call gives the same bits (the counters are left
+    zero)."""
+    q, s, b = make_layer(M + K + N, N, K, sd)
+    x = make_x(M + 5, M, K, outliers=0.01)
+    wt = upload(q, s, b, sd, gpu)
+    cols = sample_cols(N, 384, seed=K)
+    ref = O.linear_affine_f64(x, q[cols], s[cols], b[cols], sd)
+    y = _run(gpu, x, wt, kernel=2)
+    O.check_close(y[:, cols], ref, TOL, f"split gemm M={M} K={K} N={N}")
+    np.testing.assert_array_equal(_run(gpu, x, wt, kernel=2), y)
+    y0 = np.random.default_rng(M).standard_normal((M, N)).astype(np.float32)
+    ya = _run(gpu, x, wt, kernel=2, accum_into=y0)
+    O.check_close(ya[:, cols], ref + y0[:, cols], TOL, f"split gemm accum M={M} K={K} N={N}")
+
+
+def test_gemm_split_k_row_chunks(gpu):
+    """A split weight whose output tiles outnumber the workspace's 1024 counters launches in
+    chunks of rows: at the 27B down shape (K = 17408, N = 5120: 20 feature blocks, split in 2)
+    a launch takes 51 token blocks, 6528 rows. Rows on both sides of the chunk boundary give
+    the bits they give in a call of their own, which matches the oracle."""
+    import torch
+
+    from raceline_amd import ops, synth
+
+    K, N = 17408, 5120
+    M = 6528 + 300
+    mlx = synth.random_affine(N, K, 91, gpu, packed=False)
+    pw = ops.pack_affine(*mlx)
+    x = synth.random_activations(M, K, 92, gpu, outliers=0.01)
+    y = ops.linear(x, pw, kernel=2)
+    r0, r1 = 6400, 6700
+    y_sub = ops.linear(x[r0:r1].contiguous(), pw, kernel=2)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y_sub.cpu().numpy(), y[r0:r1].cpu().numpy())
+    cols = sample_cols(N, 128, seed=93)
+    w, sc, bi = mlx
+    idx = torch.as_tensor(cols, device=gpu)
+    q = O.unpack_nibbles_u32(w.index_select(0, idx).cpu().numpy().view(np.uint32))
+    sb = sc.index_select(0, idx).cpu().view(torch.int16).numpy().view(np.uint16)
+    bb = bi.index_select(0, idx).cpu().view(torch.int16).numpy().view(np.uint16)
+    ref = O.linear_affine_f64(x[r0:r1].cpu().numpy(), q, sb, bb, "f16")
+    O.check_close(y_sub.cpu().numpy()[:, cols], ref, TOL, "split gemm across a row chunk boundary")
 
 
 @pytest.mark.parametrize("K,N", [(17024, 512), (17472, 40), (17408, 1000)])   # K split in 7; 266 and 273 groups; ragged N

@@ -47,6 +47,8 @@ constexpr int kStages = 3;                  // loads run two group pairs ahead o
 constexpr int kGroupM = 4;                  // token blocks per group of the workgroup order
 constexpr int kBiasChunk = 32;              // bias product: steps of group-sum pieces staged at a time
 constexpr int kMaxGemmSplit = 2;            // workgroups per output tile when K is split
+constexpr int kProBiasSteps = 11;           // bias steps run in the prologue (their pieces fill 47 KB)
+static_assert(kGM * (32 * kProBiasSteps + 16) <= kABytes + kBBytes, "the prologue's bias pieces fit stage 2");
 // LDS by part, then stage: the three activation tiles, the three code parts, the three
 // scale parts, so that with the stage known at compile time every read of a stage is a
 // lane's base address plus an immediate offset
@@ -294,6 +296,14 @@ __device__ __forceinline__ void read_pair_head(const unsigned char *lds, uint32_
 }
 
 
+// Where byte `pos` of a chunk of bias pieces lives in the LDS: from the start at the end of
+// the kernel; in the prologue the first 32 KB in stage 2's activation part and the rest in
+// its code part (both free until stage 2 is issued). (A lambda inside the kernel here made
+// the host pass drop the kernel's launch stubs without a diagnostic.)
+__device__ __forceinline__ int bias_piece_at(int pos, bool pro) {
+  return !pro ? pos : pos < kABytes ? a_part(2) + pos : b_part(2) + (pos - kABytes);
+}
+
 // A fragment of step j of a pair (see gemm4_kernel): token tile 2 ((j >> 3) & 1) + (j & 1),
 // 32 rows of 256 bytes apart per tile, chunk of step (j >> 1) & 3 of group j >> 4.
 template <int STAGE>
@@ -399,12 +409,87 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   u32x4 wq[2];
   uint32_t sp[2] = {0u, 0u};
 
+  // Affine: acc += sum_g b[n][g] * gsum[m][g], an MFMA product over K' = P G, each group
+  // sum as P pieces (gemm_prep_kernel); a split K shares its steps out evenly over the splits
+  // (each split adds its share; any division covers every step once). Step st covers
+  // k' = 16 st .. +15; lane half h holds k' 16 st + 8 h .. +7: for fp16 biases (P = 2) the
+  // (hi, lo) of groups 8 st + 4 h .. +3, so b of those groups, each twice; for bf16 biases
+  // (P = 4) the pieces of groups 4 st + 2 h and + 1, so b of those two, four times each.
+  // Every wave needs the pieces of all 128 rows, so they go through the LDS: LDS-DMA'd once
+  // per workgroup, cs steps at a time, rows padded by 16 bytes (an odd number of 16-byte
+  // slots apart, so the fragment reads of 32 rows spread over the banks). Each wave's scale
+  // quads (its own biases) come straight from memory, in flight while the pieces land.
+  // The first kProBiasSteps steps run in the prologue, their loads in flight with the first
+  // two stages' (one wait for both), the pieces in stage 2's activation and code parts, free
+  // until stage 2 is issued: as the workgroup's last phase the bias product cost the whole
+  // round trip of its loads (27B gate_up at M = 2048: 116 us of 865). Later steps (long K,
+  // bf16 biases) run at the end, from the start of the LDS.
+  const int bsteps = a.gs_stride / 16;
+  const int st_lo = split * bsteps / S, st_hi = (split + 1) * bsteps / S;
+  const int st_pro = BOOK == kAffine ? min(st_hi, st_lo + kProBiasSteps) : st_lo;
+  auto bias_chunk = [&](int st0, int cs, bool pro) {
+    const int tn = t0 + 2 * wave;
+    const int tv = max(0, min(T, tn + 2) - tn);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sb + (size_t)min(tn, T) * G4 * 16, (uint32_t)tv * G4 * 256u);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.gs, (uint32_t)((size_t)a.M * a.gs_stride * 2));
+    const int rowb = 32 * cs + 16;                         // LDS bytes per row
+    u32x4 v[kBiasChunk];
+#pragma unroll
+    for (int u = 0; u < kBiasChunk; ++u) {
+      const int q = SD == 0 ? 2 * (st0 + u) + h : st0 + u;   // quad of groups 4q .. 4q+3
+      const uint32_t off = u < cs && q < G4 ? (uint32_t)tt * G4 * 256u + (uint32_t)q * 256u + 16u * cr : kFarOffset;
+      v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0): this wave's LDS reads are done
+    asm volatile("s_barrier" ::: "memory");               // and every wave's
+    // 1 KB blocks of the chunk (128 rows of rowb bytes), each lane 16 bytes; pad slots and
+    // rows past M read zeros
+    const int nblk = (kGM * rowb + 1023) / 1024;
+    for (int blk = wave; blk < nblk; blk += kGThreads / 64) {
+      const int pos = blk * 1024 + 16 * lane, row = pos / rowb, col = pos - row * rowb;
+      const bool ok = row < kGM && col < 32 * cs && m0 + row < a.M;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rg, lds_at(lds, bias_piece_at(blk * 1024, pro)), 16,
+          ok ? (uint32_t)(((size_t)(m0 + row) * a.gs_stride + 16 * st0) * 2 + col) : kFarOffset, 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);                        // the pieces (and the scale quads) landed
+    asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < kBiasChunk; ++u) {
+      if (u >= cs) continue;                              // uniform
+      u32x4 d;
+      if constexpr (SD == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d[e] = (v[u][e] >> 16) * 0x10001u;       // (b, b): times hi and lo
+      } else {
+        const uint32_t b0 = (h ? v[u][2] : v[u][0]) >> 16, b1 = (h ? v[u][3] : v[u][1]) >> 16;
+        d[0] = d[1] = b0 * 0x10001u;                                         // b of group 4q + 2h, four times
+        d[2] = d[3] = b1 * 0x10001u;                                         // and of group 4q + 2h + 1
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const u32x4 ag = *reinterpret_cast<const u32x4 *>(lds + bias_piece_at((mt * 32 + c32) * rowb + 32 * u + 16 * h, pro));
+        if constexpr (SD == 0)
+          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, ag),
+                                                          __builtin_bit_cast(half8, d), acc[mt], 0, 0, 0);
+        else
+          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ag),
+                                                           __builtin_bit_cast(bf16x8, d), acc[mt], 0, 0, 0);
+      }
+    }
+  };
+
   // Every stage issue loads a real pair: past the last pair the index is clamped (a
   // duplicate of the last pair into a stage nobody reads any more), so exactly two
   // stages are always in flight and one wait count fits every hand-over.
   issue_stage(src, lds, pb, 0);
   issue_stage(src, lds, pb + min(1, NPs - 1), 1);
-  __builtin_amdgcn_s_waitcnt(0x0F78);                     // vmcnt(8): stage 0 in place, 1 may fly
+  if (st_pro > st_lo) {                                   // uniform: affine with bias steps here
+    bias_chunk(st_lo, st_pro - st_lo, true);              // waits for both stages too
+    __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0): the chunk's reads are done
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x0F78);                   // vmcnt(8): stage 0 in place, 1 may fly
+  }
   asm volatile("s_barrier" ::: "memory");
   issue_stage(src, lds, pb + min(2, NPs - 1), 2);
   read_pair_head<BOOK, 0>(lds, boff, soff, pb, wq, sp);
@@ -483,73 +568,10 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
     }
   }
 
-  if (BOOK == kAffine) {
-    // acc += sum_g b[n][g] * gsum[m][g]: an MFMA product over K' = P G, each group sum as P
-    // pieces (gemm_prep_kernel); a split K shares its steps out evenly over the splits (each
-    // split adds its share; any division covers every step once). Step st covers
-    // k' = 16 st .. +15; lane half h holds k'
-    // 16 st + 8 h .. +7: for fp16 biases (P = 2) the (hi, lo) of groups 8 st + 4 h .. +3, so
-    // b of those groups, each twice; for bf16 biases (P = 4) the pieces of groups
-    // 4 st + 2 h and + 1, so b of those two, four times each. Every wave needs the pieces of
-    // all 128 rows, so they go through the LDS, which the ring no longer uses: LDS-DMA'd
-    // once per workgroup, kBiasChunk steps at a time, rows padded by 16 bytes (an odd
-    // number of 16-byte slots apart, so the fragment reads of 32 rows spread over the
-    // banks). Each wave's scale quads (its own biases) come straight from memory, in flight
-    // while the pieces land.
-    const int tn = t0 + 2 * wave;
-    const int tv = max(0, min(T, tn + 2) - tn);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sb + (size_t)min(tn, T) * G4 * 16, (uint32_t)tv * G4 * 256u);
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.gs, (uint32_t)((size_t)a.M * a.gs_stride * 2));
-    const int steps = a.gs_stride / 16;
-    const int st_lo = split * steps / S, st_hi = (split + 1) * steps / S;
-    for (int st0 = st_lo; st0 < st_hi; st0 += kBiasChunk) {
-      const int cs = min(kBiasChunk, st_hi - st0);
-      const int rowb = 32 * cs + 16;                       // LDS bytes per row
-      u32x4 v[kBiasChunk];
-#pragma unroll
-      for (int u = 0; u < kBiasChunk; ++u) {
-        const int q = SD == 0 ? 2 * (st0 + u) + h : st0 + u;   // quad of groups 4q .. 4q+3
-        const uint32_t off = u < cs && q < G4 ? (uint32_t)tt * G4 * 256u + (uint32_t)q * 256u + 16u * cr : kFarOffset;
-        v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
-      }
-      __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0): this wave's LDS reads are done
-      asm volatile("s_barrier" ::: "memory");               // and every wave's
-      // 1 KB blocks of the chunk (128 rows of rowb bytes), each lane 16 bytes; pad slots and
-      // rows past M read zeros
-      const int nblk = (kGM * rowb + 1023) / 1024;
-      for (int blk = wave; blk < nblk; blk += kGThreads / 64) {
-        const int pos = blk * 1024 + 16 * lane, row = pos / rowb, col = pos - row * rowb;
-        const bool ok = row < kGM && col < 32 * cs && m0 + row < a.M;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rg, lds_at(lds, blk * 1024), 16,
-            ok ? (uint32_t)(((size_t)(m0 + row) * a.gs_stride + 16 * st0) * 2 + col) : kFarOffset, 0, 0, 0);
-      }
-      __builtin_amdgcn_s_waitcnt(0);                        // the pieces (and the scale quads) landed
-      asm volatile("s_barrier" ::: "memory");
-#pragma unroll
-      for (int u = 0; u < kBiasChunk; ++u) {
-        if (u >= cs) continue;                              // uniform
-        u32x4 d;
-        if constexpr (SD == 0) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) d[e] = (v[u][e] >> 16) * 0x10001u;       // (b, b): times hi and lo
-        } else {
-          const uint32_t b0 = (h ? v[u][2] : v[u][0]) >> 16, b1 = (h ? v[u][3] : v[u][1]) >> 16;
-          d[0] = d[1] = b0 * 0x10001u;                                         // b of group 4q + 2h, four times
-          d[2] = d[3] = b1 * 0x10001u;                                         // and of group 4q + 2h + 1
-        }
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const u32x4 ag = *reinterpret_cast<const u32x4 *>(lds + (mt * 32 + c32) * rowb + 32 * u + 16 * h);
-          if constexpr (SD == 0)
-            acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, ag),
-                                                            __builtin_bit_cast(half8, d), acc[mt], 0, 0, 0);
-          else
-            acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ag),
-                                                             __builtin_bit_cast(bf16x8, d), acc[mt], 0, 0, 0);
-        }
-      }
-    }
+  if constexpr (BOOK == kAffine) {
+    // the bias steps the prologue left (long K, bf16 biases): the LDS from its start, which
+    // the ring no longer uses
+    for (int st0 = st_pro; st0 < st_hi; st0 += kBiasChunk) bias_chunk(st0, min(kBiasChunk, st_hi - st0), false);
   }
 
   // D of a 32x32 tile: lane l holds column l%32, rows 8 (v/4) + 4 (l/32) + v%4. acc becomes

@@ -220,45 +220,77 @@ __device__ int block_exclusive_scan(int v, int *wave_tot, int *total) {
   return ex;
 }
 
+// A workgroup barrier that orders LDS accesses only: __syncthreads also waits for every
+// global store in flight (its release fence), which the sort's later phases never read back
+// (the work items, rows and slots are for the next kernels); that wait took about 1 us at
+// each such barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);             // lgkmcnt(0): this thread's LDS accesses are done
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // One workgroup of 1024 threads sorts all T*S assignments by expert (a counting sort,
 // moe.metal:109-139) and writes the work list. Within an expert, rows follow token order:
-// token t's row for expert e is off[e] + (tokens before t that chose e), counted with one
-// bitmap per expert over a chunk of tokens and prefix popcounts (a token chooses an expert
-// at most once). LDS: counts and offsets, then per chunk bm[E+1][wpe] and pre[E+1][wpe].
-__device__ void sort_assignments(const int *sel, int T, int E, int S, int wpe, int *tok, int *inv, int4 *items,
+// token t's row for expert e is off[e] + (tokens before t that chose e). The tokens go in
+// rounds of 64 per wave (wpr waves): lane i of wave w holds token 64 w + i of the round and
+// sets bit i of its wave's 64-bit mask of each expert it chose, so within the wave a token's
+// rank is a popcount of the lower lanes' bits and the wave's count for the expert the
+// popcount of the mask (a token chooses an expert at most once). Pass 1 adds every wave's
+// counts into the experts' totals, a scan gives the row offsets and the work items; pass 2
+// turns each round's per-wave counts into per-wave row bases (expert by expert, in wave
+// order) and places every assignment. With one round (T <= 64 wpr) pass 2 reuses pass 1's
+// masks and each lane keeps its token's experts in registers.
+// LDS: off[1024], scan scratch[32], cnt[wpr][E+1] ints, then mask[wpr][E+1] 64-bit words.
+__device__ void sort_assignments(const int *sel, int T, int E, int S, int wpr, int *tok, int *inv, int4 *items,
                                  int *n_items, unsigned char *lds) {
-  int *cnt = reinterpret_cast<int *>(lds);      // [1024]
-  int *off = cnt + 1024;                        // [1024]
-  int *run = off + 1024;                        // [1024]
-  int *scratch = run + 1024;                    // [32]
-  uint32_t *bm = reinterpret_cast<uint32_t *>(scratch + 32);   // [(E+1) * wpe]
-  uint32_t *pre = bm + (size_t)(E + 1) * wpe;                   // [(E+1) * wpe]
-  const int tid = threadIdx.x;
-  const int A = T * S;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E1 = E + 1;
+  int *off = reinterpret_cast<int *>(lds);      // [1024]: totals, then row offsets / running bases
+  int *scratch = off + 1024;                    // [32]
+  int *cnt = scratch + 32;                      // [wpr][E1]
+  uint64_t *mask = reinterpret_cast<uint64_t *>(lds + ((size_t)(1056 + wpr * E1) * 4 + 7) / 8 * 8);   // [wpr][E1]
+  const int per_round = 64 * wpr, rounds = (T + per_round - 1) / per_round;
+  const bool in_round = wave < wpr;
+  uint64_t *my_mask = mask + (size_t)wave * E1;
+  int *my_cnt = cnt + (size_t)wave * E1;
+  int ev[kMaxTopk + 1];                         // this lane's token's experts (sel is clamped into 0..E)
 
-  cnt[tid] = 0;
-  run[tid] = 0;
-  // sel comes from moe_topk_kernel (0 <= sel < E + 1); the clamps keep every index in
-  // range whatever it holds. The first kSortCached assignments of each thread stay in
-  // registers for the later passes (the one-chunk case: all of them up to A = 8192).
-  constexpr int kSortCached = 8;
-  int sv[kSortCached];
+  // the masks of round r for this wave: zeroed, then every chosen expert's bit of each lane
+  auto build = [&](int r) {
+    for (int e = lane; e < E1; e += 64) my_mask[e] = 0ull;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int t = r * per_round + 64 * wave + lane;
 #pragma unroll
-  for (int i = 0; i < kSortCached; ++i) {
-    const int a = tid + 1024 * i;
-    sv[i] = a < A ? min(max(sel[a], 0), E) : 0;
+    for (int k = 0; k <= kMaxTopk; ++k) {
+      if (k >= S) break;                        // uniform
+      ev[k] = t < T ? min(max(sel[(size_t)t * S + k], 0), E) : 0;
+      if (t < T) atomicOr(reinterpret_cast<unsigned long long *>(my_mask + ev[k]), 1ull << lane);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // pass 1: the experts' totals
+  off[tid] = 0;
+  lds_barrier();
+  for (int r = 0; r < rounds; ++r) {
+    if (in_round) {
+      build(r);
+      for (int e = lane; e < E1; e += 64) {
+        const int c = __popcll(my_mask[e]);
+        my_cnt[e] = c;
+        if (c) atomicAdd(&off[e], c);
+      }
+    }
   }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kSortCached; ++i)
-    if (tid + 1024 * i < A) atomicAdd(&cnt[sv[i]], 1);
-  for (int a = tid + 1024 * kSortCached; a < A; a += 1024) atomicAdd(&cnt[min(max(sel[a], 0), E)], 1);
-  __syncthreads();
-  const int c = tid < E1 ? cnt[tid] : 0;
+  lds_barrier();
+  const int c = tid < E1 ? off[tid] : 0;
   const int ni = (c + kItemRows - 1) / kItemRows;
   int o, io, n_it;
-  if (A < (1 << 15)) {   // uniform: counts and item counts fit one scan, 16 bits each
+  if ((long long)T * S < (1 << 15)) {   // uniform: counts and item counts fit one scan, 16 bits each
     const int packed = block_exclusive_scan(c | (ni << 16), scratch, scratch + 16);
     o = packed & 0xFFFF;
     io = packed >> 16;
@@ -274,64 +306,51 @@ __device__ void sort_assignments(const int *sel, int T, int E, int S, int wpe, i
       items[io + i] = int4{tid, o + i * kItemRows, min(kItemRows, c - i * kItemRows), 0};
   }
   if (tid == 0) *n_items = n_it;
-  __syncthreads();
+  lds_barrier();
 
-  const int chunk = 32 * wpe;                   // tokens per chunk
-  // an assignment's expert: from registers in the one-chunk case (chunk 0 starts at a = 0,
-  // so the k-th assignment a thread visits is its k-th cached one), else from memory
-  const bool cached = T <= chunk && A <= 1024 * kSortCached;   // uniform
-  auto expert_of = [&](int a, int k) {
-    int e = 0;
-#pragma unroll
-    for (int i = 0; i < kSortCached; ++i) e = i == k ? sv[i] : e;
-    return cached ? e : min(max(sel[a], 0), E);
-  };
-  for (int t0 = 0; t0 < T; t0 += chunk) {
-    const int tn = min(chunk, T - t0);
-    const int nw = (tn + 31) / 32;              // bitmap words in use per expert
-    for (int i = tid; i < E1 * wpe; i += 1024) bm[i] = 0u;
-    __syncthreads();
-    for (int a = t0 * S + tid, k = 0; a < (t0 + tn) * S; a += 1024, ++k) {
-      const int tl = a / S - t0;
-      atomicOr(&bm[(size_t)expert_of(a, k) * wpe + (tl >> 5)], 1u << (tl & 31));
+  // pass 2: each round's per-wave row bases, then the rows
+  for (int r = 0; r < rounds; ++r) {
+    if (rounds > 1) {                           // uniform: one round keeps pass 1's masks and counts
+      if (in_round) {
+        build(r);
+        for (int e = lane; e < E1; e += 64) my_cnt[e] = __popcll(my_mask[e]);
+      }
+      lds_barrier();
     }
-    __syncthreads();
     if (tid < E1) {
-      // running popcounts over the expert's words, eight words read at a time
-      uint32_t acc = 0;
-      for (int i0 = 0; i0 < nw; i0 += 8) {
-        uint32_t wv[8];
+      // every wave's count is read before the first base is written (one LDS round trip)
+      int cw[16];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) wv[i] = i0 + i < nw ? bm[(size_t)tid * wpe + i0 + i] : 0u;
+      for (int w = 0; w < 16; ++w) cw[w] = w < wpr ? cnt[(size_t)w * E1 + tid] : 0;
+      int run = off[tid];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          if (i0 + i < nw) pre[(size_t)tid * wpe + i0 + i] = acc;
-          acc += __popc(wv[i]);
-        }
+      for (int w = 0; w < 16; ++w) {
+        if (w < wpr) cnt[(size_t)w * E1 + tid] = run;
+        run += cw[w];
+      }
+      off[tid] = run;                           // the next round continues the expert's rows
+    }
+    lds_barrier();
+    const int t = r * per_round + 64 * wave + lane;
+    if (in_round && t < T) {
+      const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+      for (int k = 0; k <= kMaxTopk; ++k) {
+        if (k >= S) break;                      // uniform
+        const int e = ev[k];
+        const int pos = my_cnt[e] + __popcll(my_mask[e] & below);
+        inv[(size_t)t * S + k] = pos;
+        tok[pos] = t;
       }
     }
-    __syncthreads();
-    for (int a = t0 * S + tid, k = 0; a < (t0 + tn) * S; a += 1024, ++k) {
-      const int t = a / S, tl = t - t0, e = expert_of(a, k);
-      const size_t wi = (size_t)e * wpe + (tl >> 5);
-      const int rank = run[e] + (int)pre[wi] + __popc(bm[wi] & ((1u << (tl & 31)) - 1u));
-      const int pos = off[e] + rank;
-      inv[a] = pos;
-      tok[pos] = t;
-    }
-    if (t0 + chunk < T) {   // uniform: a later chunk continues each expert's rows
-      __syncthreads();
-      if (tid < E1)
-        run[tid] += (int)(pre[(size_t)tid * wpe + nw - 1] + __popc(bm[(size_t)tid * wpe + nw - 1]));
-      __syncthreads();
-    }
+    if (r + 1 < rounds) lds_barrier();        // uniform: the next round rebuilds masks and counts
   }
 }
 
-__global__ __launch_bounds__(1024) void moe_sort_kernel(const int *sel, int T, int E, int S, int wpe, int *tok,
+__global__ __launch_bounds__(1024) void moe_sort_kernel(const int *sel, int T, int E, int S, int wpr, int *tok,
                                                         int *inv, int4 *items, int *n_items) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  sort_assignments(sel, T, E, S, wpe, tok, inv, items, n_items, lds);
+  sort_assignments(sel, T, E, S, wpr, tok, inv, items, n_items, lds);
 }
 
 // The sort for a few assignments (A <= 1024, one thread each): an assignment's row within its
@@ -866,8 +885,14 @@ static int launch_expert(int K, int sd, int tpe, int items, int tokens, hipStrea
                        : launch_expert_inst<24, 1, KIND>(grid, threads, st, a);
 }
 
-static size_t sort_lds_bytes(int E, int wpe) { return (3 * 1024 + 32) * 4 + (size_t)2 * (E + 1) * wpe * 4; }
-static int sort_wpe(int E) { return std::max(1, std::min(32, 8192 / (E + 1))); }
+// the sort's waves per round of tokens: 16, or as many as the LDS holds (12 bytes per wave
+// and expert)
+static size_t sort_lds_bytes(int E, int wpr) { return ((size_t)(1056 + wpr * (E + 1)) * 4 + 7) / 8 * 8 + (size_t)wpr * (E + 1) * 8; }
+static int sort_wpr(int E) {
+  int w = 16;                                   // at most 16 (the sort's per-expert pass holds 16 counts)
+  while (w > 1 && sort_lds_bytes(E, w) > 160 * 1024) --w;
+  return w;
+}
 
 static int check_moe_shape(const char *fn, int T, int E, int topk, int H, int I) {
   RLQ_REQUIRE(T >= 1 && E >= 1 && E <= kMaxExperts, "%s: T=%d E=%d (1 <= E <= %d)", fn, T, E, kMaxExperts);
@@ -1218,8 +1243,8 @@ int rlq_moe_route(const float *logits, int logit_stride, int T, int E, int topk,
   RLQ_REQUIRE(aligned(items, 16), "rlq_moe_route: items must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int epl = (E + 63) / 64;
-  const int wpe = sort_wpe(E);
-  const size_t lds = sort_lds_bytes(E, wpe);
+  const int wpr = sort_wpr(E);
+  const size_t lds = sort_lds_bytes(E, wpr);
   if (T <= kRouteSmallTokens) {
     // one launch: the top-k of each token by its own wave, then the sort (8 KB of LDS)
     int4 *it4 = reinterpret_cast<int4 *>(items);
@@ -1244,7 +1269,7 @@ int rlq_moe_route(const float *logits, int logit_stride, int T, int E, int topk,
   RLQ_HIP(hipGetLastError());
   static LdsOptIn lds_opt;
   if (int rc = allow_large_lds(reinterpret_cast<const void *>(&moe_sort_kernel), lds_opt)) return rc;
-  moe_sort_kernel<<<1, 1024, lds, st>>>(sel, T, E, topk + 1, wpe, tok, inv, reinterpret_cast<int4 *>(items), n_items);
+  moe_sort_kernel<<<1, 1024, lds, st>>>(sel, T, E, topk + 1, wpr, tok, inv, reinterpret_cast<int4 *>(items), n_items);
   RLQ_HIP(hipGetLastError());
   return 0;
 }

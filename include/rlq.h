@@ -83,10 +83,12 @@ int rlq_repack_blocked(const uint8_t *w_blk, const uint16_t *s_blk, const uint16
 /* Bytes of scratch rlq_linear_affine and rlq_linear_native need for these sizes (and for
  * any smaller M). The first 4096 bytes hold the decode kernel's counters for weights whose
  * K it splits across workgroups (few tiles, long K: the down projections); they must be
- * zero before the workspace's first use, and every call leaves them zero. The rest holds
- * the decode kernel's partial sums for such weights, or the prefill kernel's prepared
- * activations and group sums (and, for a weight whose K it splits in two, K >= 2N, the
- * second half's partial products), and is not kept between calls. Calls that share one
+ * zero before the workspace's first use, and every call leaves them zero; the prefill
+ * kernel counts in the same bytes for weights whose K it splits in two (at most 32 blocks of
+ * 256 outputs and 64 pairs of groups or more, such as the 27B down projection). The rest
+ * holds the decode kernel's partial sums for such weights, or the prefill kernel's prepared
+ * activations and group sums (and, for a weight whose K it splits, the second half's
+ * partial products), and is not kept between calls. Calls that share one
  * workspace must not overlap. Pass NULL and 0 only where this query returns 0. */
 size_t rlq_linear_workspace_bytes(int M, int K, int N);
 

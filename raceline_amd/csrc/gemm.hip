@@ -55,6 +55,11 @@ static_assert(kGM * (32 * kProBiasSteps + 16) <= kABytes + kBBytes, "the prologu
 constexpr int a_part(int stage) { return stage * kABytes; }
 constexpr int b_part(int stage) { return kStages * kABytes + stage * kBBytes; }
 constexpr int s_part(int stage) { return kStages * (kABytes + kBBytes) + stage * kSBytes; }
+// affine: the tile's 128 row scales 2^-e, after the ring (read by the stores at the end);
+// 1 KB, as the one LDS-DMA that brings them writes 16 bytes for each of the 64 lanes
+constexpr int kRscaleLds = kStages * kStageBytes;
+constexpr int kGemmLdsBytes = kRscaleLds + 1024;
+static_assert(kGemmLdsBytes <= 160 * 1024, "the row scales fit after the ring");
 
 // ------------------------------------------------------------------ affine prep pass
 
@@ -482,6 +487,12 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
   // Every stage issue loads a real pair: past the last pair the index is clamped (a
   // duplicate of the last pair into a stage nobody reads any more), so exactly two
   // stages are always in flight and one wait count fits every hand-over.
+  if (BOOK == kAffine && wave == 0) {
+    // the tile's row scales, first in wave 0's queue, so every wait below covers them
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.rscale + m0, (uint32_t)(min(kGM, a.M - m0) * 4));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, lds_at(lds, kRscaleLds), 16, lane < 32 ? 16u * lane : kFarOffset, 0,
+                                             0, 0);
+  }
   issue_stage(src, lds, pb, 0);
   issue_stage(src, lds, pb + min(1, NPs - 1), 1);
   if (st_pro > st_lo) {                                   // uniform: affine with bias steps here
@@ -586,7 +597,8 @@ __global__ __launch_bounds__(kGThreads) void gemm4_kernel(GemmArgs a) {
       const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
       if (col && m < a.M) {
         float val = acc[mt][v];
-        if constexpr (BOOK == kAffine) val *= a.rscale[m];   // undoes the prep's 2^e, exactly
+        if constexpr (BOOK == kAffine)   // undoes the prep's 2^e, exactly (the scale staged in the prologue)
+          val *= reinterpret_cast<const float *>(lds + kRscaleLds)[m - m0];
         if constexpr (BOOK == kInt16) {
           if (split == 0) val = __builtin_fmaf(0.5f, a.asum[m], val);
         }
@@ -764,7 +776,7 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
   a.cnt = cnt;
   if (S > 1) a.y_part = reinterpret_cast<float *>(static_cast<char *>(ws) + books_workspace(book, M, K));
   const int nblocks = (N + kGN - 1) / kGN;
-  const size_t lds = (size_t)kStages * kStageBytes;
+  const size_t lds = (size_t)kGemmLdsBytes;
   // a split weight launches in chunks of rows whose tiles have counters; the rows are
   // independent, so chunking changes no result
   const int chunk = S > 1 ? split_chunk_rows(N) : M;

@@ -125,14 +125,15 @@ __device__ __forceinline__ void write_gs_pieces(uint16_t *gs, int gs_stride, int
     for (int k = P * G; k < gs_stride; ++k) gs[(size_t)m * gs_stride + k] = 0;
 }
 
-// The workgroup's max |x| of its row from each thread's partial max.
+// The workgroup's max |x| of its row from each thread's partial max (THR threads).
+template <int THR = kPrepThreads>
 __device__ __forceinline__ float row_max(float mx, float *wmax) {
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, d));
   if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
   __syncthreads();
 #pragma unroll
-  for (int w = 0; w < kPrepThreads / 64; ++w) mx = __builtin_fmaxf(mx, wmax[w]);
+  for (int w = 0; w < THR / 64; ++w) mx = __builtin_fmaxf(mx, wmax[w]);
   return mx;
 }
 
@@ -148,14 +149,16 @@ __device__ __forceinline__ int row_exponent(float mx) {
   return ex;
 }
 
-// The prep pass with the row read once: thread i holds chunks i, i + 256, ... (CPT of
-// them, K <= 2048 CPT) in registers between the max and the writes. The same arithmetic in
-// the same order as gemm_prep_kernel below, so the same bits.
-template <int SD, int CPT>
-__global__ __launch_bounds__(kPrepThreads) void gemm_prep1_kernel(const _Float16 *x, int x_stride, int M, int K,
-                                                                  _Float16 *xp, uint16_t *gs, int gs_stride,
-                                                                  float *rscale) {
-  __shared__ float wmax[kPrepThreads / 64];
+// The prep pass with the row read once: thread i of THR holds chunks i, i + THR, ... (CPT of
+// them, K <= 8 THR CPT) in registers between the max and the writes. The same arithmetic in
+// the same order as gemm_prep_kernel below, so the same bits (the max does not depend on the
+// order, and each group's sum is its 8 threads' fixed butterfly whatever THR is). Rows of more
+// than 8192 activations take 1024 threads: with 256 threads, 16 chunks each held 154 VGPRs
+// (3 waves per SIMD), and the 27B down projection's prep (K = 17408) ran at 4.1 TB/s.
+template <int SD, int CPT, int THR = kPrepThreads>
+__global__ __launch_bounds__(THR) void gemm_prep1_kernel(const _Float16 *x, int x_stride, int M, int K,
+                                                         _Float16 *xp, uint16_t *gs, int gs_stride, float *rscale) {
+  __shared__ float wmax[THR / 64];
   const int m = blockIdx.x;
   const int C = K / 8;                                  // chunks per row (a multiple of 8)
   const _Float16 *row = x + (size_t)m * x_stride;
@@ -163,21 +166,21 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep1_kernel(const _Float16
   float mx = 0.0f;
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
-    const int c = threadIdx.x + kPrepThreads * j;
+    const int c = threadIdx.x + THR * j;
     v[j] = c < C ? *reinterpret_cast<const u32x4 *>(row + 8 * c) : u32x4{};
     const half8 h = __builtin_bit_cast(half8, v[j]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) mx = __builtin_fmaxf(mx, __builtin_fabsf(static_cast<float>(h[e])));
   }
-  mx = row_max(mx, wmax);
+  mx = row_max<THR>(mx, wmax);
   const int ex = row_exponent(mx);
   const float f = __builtin_ldexpf(1.0f, ex);
   if (threadIdx.x == 0) rscale[m] = __builtin_ldexpf(1.0f, -ex);
   const int G = C >> 3;
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
-    if (kPrepThreads * j >= C) break;                   // uniform: the butterfly needs every lane
-    const int c = threadIdx.x + kPrepThreads * j;
+    if (THR * j >= C) break;                   // uniform: the butterfly needs every lane
+    const int c = threadIdx.x + THR * j;
     const half8 h = __builtin_bit_cast(half8, v[j]);
     float sum = 0.0f;
 #pragma unroll
@@ -749,13 +752,12 @@ int run_gemm4(int book, const _Float16 *x, int x_stride, int M, int K, int N, co
     float *rscale = reinterpret_cast<float *>(static_cast<char *>(ws) + xp_bytes +
                                               ((size_t)M * gs_stride_of(G, 1) * 2 + 255) / 256 * 256);
     const int cpt = (K / 8 + kPrepThreads - 1) / kPrepThreads;   // chunks of the row per thread
-#define RLQ_PREP(KERNEL, ...)                                                                                          \
-  (sd == RLQ_BF16 ? KERNEL<1, ##__VA_ARGS__><<<M, kPrepThreads, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale) \
-                  : KERNEL<0, ##__VA_ARGS__><<<M, kPrepThreads, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale))
-    if (cpt <= 4) RLQ_PREP(gemm_prep1_kernel, 4);
-    else if (cpt <= 8) RLQ_PREP(gemm_prep1_kernel, 8);
-    else if (cpt <= 16) RLQ_PREP(gemm_prep1_kernel, 16);
-    else RLQ_PREP(gemm_prep_kernel);
+#define RLQ_PREP(THR, KERNEL, ...)                                                                                     \
+  (sd == RLQ_BF16 ? KERNEL<1, ##__VA_ARGS__><<<M, THR, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale)          \
+                  : KERNEL<0, ##__VA_ARGS__><<<M, THR, 0, st>>>(x, x_stride, M, K, xp, gs, gs_stride, rscale))
+    if (cpt <= 4) RLQ_PREP(kPrepThreads, gemm_prep1_kernel, 4);
+    else if (cpt <= 16) RLQ_PREP(1024, gemm_prep1_kernel, 4, 1024);   // K <= 32768: 4 chunks per thread of 1024
+    else RLQ_PREP(kPrepThreads, gemm_prep_kernel);
 #undef RLQ_PREP
     RLQ_HIP(hipGetLastError());
     a.x = xp; a.x_stride = K; a.gs = gs; a.gs_stride = gs_stride; a.rscale = rscale;

@@ -229,6 +229,31 @@ def test_repeat_calls_reuse_workspace(gpu):
         np.testing.assert_array_equal(_run(gpu, x, wt, kernel=1), first)
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 17408, 1000), (8, 17408, 1000), (150, 8192, 1024)])   # decode split in 7; prefill in 2
+def test_split_k_replays_in_a_graph(gpu, M, K, N):
+    """A call whose K is split across workgroups, captured in a graph, gives the eager call's
+    bits on every replay, with eager work on the same output and workspace between the
+    replays: every call leaves its arrival counters zero, so replays need no reset."""
+    import torch
+
+    from raceline_amd import ops, synth
+
+    pw = ops.pack_affine(*synth.random_affine(N, K, 31 + M, gpu, packed=False))
+    x = synth.random_activations(M, K, 32 + M, gpu, outliers=0.01)
+    want = ops.linear(x, pw)                       # eager; also sizes the workspace
+    out = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.linear(x, pw, out=out)
+    for _ in range(4):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        assert torch.equal(ops.linear(x, pw), want)   # an eager split call between replays
+
+
 @pytest.mark.parametrize("sd", ["f16", "bf16"])
 def test_repack_blocked_round_trip(gpu, sd):
     """.rlm blocked q4a tensor (tools/convert.py:92-117) -> MLX layout, per stacked part."""

@@ -254,6 +254,37 @@ def test_token_result_same_across_kernel_choice(gpu, E, H, I):
     O.check_close(h5.cpu().numpy().astype(np.float64), ref, TOL, "moe per-tile vs staged")
 
 
+@pytest.mark.parametrize("T", [1, 3, 70])
+def test_layer_replays_in_a_graph(gpu, T):
+    """rlq_moe captured in a graph gives the eager call's bits on every replay, with eager
+    calls on the same workspace between the replays: one token (the routing inside the
+    gate/up launch), three (the down product and the combine in one launch) and a batch
+    (top-k, sort, staged experts, combine)."""
+    import torch
+
+    from raceline_amd import ops
+
+    E, topk, H, I = 32, 4, 512, 256
+    gu, dn = make_moe(50 + T, E, H, I)
+    mw = upload_moe(gu, dn, E, H, I, "f16", gpu)
+    x, logits = make_inputs(51 + T, T, E, H)
+    xd, ld = to_dev(x, gpu), to_dev(logits, gpu)
+    h0 = to_dev(np.random.default_rng(52).standard_normal((T, H)).astype(np.float32), gpu)
+    ws = torch.empty(ops.moe_workspace_bytes(T, E, topk, H, I), dtype=torch.uint8, device=gpu)
+    want = ops.moe(xd, ld, mw, topk, h0.clone(), workspace=ws)
+    h = h0.clone()
+    _sync()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.moe(xd, ld, mw, topk, h, workspace=ws)
+    for _ in range(4):
+        h.copy_(h0)
+        g.replay()
+        _sync()
+        assert torch.equal(h, want)
+        assert torch.equal(ops.moe(xd, ld, mw, topk, h0.clone(), workspace=ws), want)
+
+
 def test_combine_one_and_four_wide_paths_agree(gpu):
     """The combine takes four floats per thread when rows and pointers allow 16-byte accesses
     and one otherwise; both follow the same per-element order, so they give the same bits,

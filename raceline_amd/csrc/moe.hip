@@ -503,7 +503,8 @@ __global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
 // One token: its routing and the gate/up products in one launch. Every workgroup picks the
 // token's experts itself (wave 0, topk_token, as moe_topk_kernel does) and takes its item
 // from them: with one token each chosen expert has one row, and the sort orders experts by
-// number, so item i (= blockIdx.y, S of them) is the i-th smallest chosen expert, at row i.
+// number, so item i (= blockIdx.y, S of them) is the i-th smallest chosen expert, at row i;
+// the shared expert, number E, is always the last, so its workgroups skip the routing.
 // Workgroup (0, 0) also writes the routing tables (sel, w, tok, inv, items, n_items) as the
 // sort writes them for one token, for the down and combine launch. LDS: the reduction, then
 // sel [S], w [S] and the chosen experts in ascending order [S].
@@ -513,6 +514,12 @@ __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, 
                                                                      int *inv, int4 *items, int *n_items) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int S = topk + 1;
+  if (blockIdx.y == S - 1 && blockIdx.y != 0) {
+    // the shared expert (number E) is the largest chosen one, so always the last item:
+    // its workgroups need no routing and stream their weights at once
+    expert_tile<GPW, SD, 0, true>(a, E, S - 1, 1, lds);
+    return;
+  }
   const int waves = blockDim.x >> 6;
   int *sel_l = reinterpret_cast<int *>(lds + (size_t)(waves - 1) * 64 * 16);
   float *w_l = reinterpret_cast<float *>(sel_l + S);
@@ -1148,6 +1155,13 @@ __global__ __launch_bounds__(1024) void moe_native_gate_up_one_token_kernel(
     float *w, int *tok, int *inv, int4 *items, int *n_items) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int S = topk + 1;
+  if (blockIdx.y == S - 1 && blockIdx.y != 0) {
+    // the shared expert (number E) is always the last item: no routing to wait for
+    const int slot = __builtin_amdgcn_readfirstlane(slots[E]);
+    native_gate_up_tile<GPW, BOOK, true>(x, x_stride, 1, nullptr, H, I, codes, s, slot, n_slots, S - 1, 1, cs, act,
+                                         act_stride, lds);
+    return;
+  }
   const int waves = blockDim.x >> 6;
   int *sel_l = reinterpret_cast<int *>(lds + (size_t)2 * (waves - 1) * 64 * 16);
   float *w_l = reinterpret_cast<float *>(sel_l + S);

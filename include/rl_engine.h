@@ -118,9 +118,13 @@ int rl_expert_cache(const rl_engine *e, unsigned long long *hits, unsigned long 
 void rl_expert_cache_size(const rl_engine *e, int *experts, unsigned long long *slot_bytes);
 
 /* The head over the draft vocabulary for one row of h (the logits part of
- * Engine::encode_mtp_layer, src/engine.mm:1419-1436): final norm, lm_head rows
+ * Engine::encode_mtp_layer, src/engine.mm:1419-1436): the RMS norm, lm_head rows
  * [0, rl_draft_main()) and, when a tail is set, rows [rl_draft_tail(), n_pad) right after
- * them: rl_draft_vocab() logits in the engine's draft logits (device memory). */
+ * them: rl_draft_vocab() logits in the engine's draft logits (device memory). The norm is
+ * the reference's for the row: mtp.norm folded with lm_head's column scales in a native
+ * file with an MTP head (src/engine.mm:534); in a file without one, final_norm (this
+ * engine's extension: the reference has no draft head there). A rotated file with an MTP
+ * head is refused (its rotation kernel is not on this path). */
 const float *rl_draft_head(rl_engine *e, const float *h_row, void *stream);
 
 /* The k largest of n logits in descending order, ties to the lowest index, NaN skipped
@@ -128,11 +132,13 @@ const float *rl_draft_head(rl_engine *e, const float *h_row, void *stream);
 int rl_top_k(const float *logits, int n, int k, int32_t *ids, float *vals);
 
 /* rl_top_k over n device logits, on the GPU: ids and vals (host) receive the result; the
- * call waits for the stream. k <= 256. Same order and ties as rl_top_k. */
+ * call waits for the stream. k <= 256, n <= 16 * rl_logits_stride() (the engine's logits
+ * buffer). Same order and ties as rl_top_k. */
 int rl_top_k_device(rl_engine *e, const float *logits, int n, int k, int32_t *ids, float *vals, void *stream);
 
 /* src/capi.h:39: the index of the largest of the first rl_vocab() logits of row 0 of the last
- * rl_head call (the lowest index among equal ones). Waits for the GPU. */
+ * rl_head call (the lowest index among equal ones). Runs on the stream that rl_head call ran
+ * on, and waits for it. */
 int rl_argmax(const rl_engine *e);
 
 #ifdef __cplusplus

@@ -182,19 +182,27 @@ __global__ __launch_bounds__(kTopkThreads) void topk_chunk_kernel(const float *x
   pick_k<kTopkPer, kTopkThreads>(v, idx, k, cand_v + (size_t)blockIdx.x * k, cand_i + (size_t)blockIdx.x * k, scratch);
 }
 
+// Pass 2 and later: workgroup b takes candidates [b G, (b+1) G) of m, G = 1024 PER, and
+// writes its k best to out + b k. The k best of a union are the k best of the groups' k
+// best, so passes repeat until one workgroup is left; every candidate keeps its index
+// into x, so the order (value, then index) is the same as one merge over all of them.
+constexpr int kTopkMergePer = 16;
+constexpr int kTopkMergeGroup = kTopkMergeThreads * kTopkMergePer;
+
 template <int PER>
 __global__ __launch_bounds__(kTopkMergeThreads) void topk_merge_kernel(const float *cand_v, const int *cand_i, int m,
                                                                        int k, float *out_v, int *out_i) {
   __shared__ Cand scratch[kTopkMergeThreads / 64];
   float v[PER];
   int idx[PER];
+  const int base = blockIdx.x * kTopkMergeThreads * PER;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int c = j * kTopkMergeThreads + threadIdx.x;
+    const int c = base + j * kTopkMergeThreads + threadIdx.x;
     v[j] = c < m ? cand_v[c] : 0.0f;
     idx[j] = c < m ? cand_i[c] : -1;
   }
-  pick_k<PER, kTopkMergeThreads>(v, idx, k, out_v, out_i, scratch);
+  pick_k<PER, kTopkMergeThreads>(v, idx, k, out_v + (size_t)blockIdx.x * k, out_i + (size_t)blockIdx.x * k, scratch);
 }
 
 // ------------------------------------------------------------------ the engine
@@ -217,10 +225,13 @@ struct rl_engine {
   std::map<std::string, rlq::DevMem> floats;     // f32 tensors as they are in the file
   std::vector<rlq::DevMem> norm_in, norm_post;   // native: folded norm weights per layer
   rlq::DevMem norm_final;
+  rlq::DevMem norm_mtp_out;                      // native files with an MTP head: mtp.norm folded with lm_head's column scales
+  bool has_mtp = false;
   int x_stride = 0, proj_stride = 0, act_stride = 0, router_stride = 0;
   rlq::DevMem xn, proj, act, router_logits, linear_ws, moe_ws, logits, draft_logits, slots;
-  rlq::DevMem topk_v, topk_i, topk_out_v, topk_out_i;
+  rlq::DevMem topk_v, topk_i, topk_v2, topk_i2, topk_out_v, topk_out_i;
   int head_rows_done = 0;                        // rows of the last rl_head
+  hipStream_t head_stream = nullptr;             // the stream the last rl_head ran on
   int draft_vocab_rows = 0, draft_tail_first = -1;
 };
 
@@ -376,6 +387,13 @@ static int open_engine(rl_engine *e, const char *path, int max_ctx, int max_chun
     }
     if (const FTensor *ff = e->model->f("final_norm"))
       if (int rc = fold_norm(e, e->norm_final, *ff, e->model->q("lm_head"))) return rc;
+    // the MTP head's output norm, folded as src/engine.mm:534 does (has_mtp_: native files
+    // with mtp.fc, :398)
+    const FTensor *fm = e->model->f("mtp.norm");
+    if (e->model->q("mtp.fc") && fm) {
+      if (int rc = fold_norm(e, e->norm_mtp_out, *fm, e->model->q("lm_head"))) return rc;
+      e->has_mtp = true;
+    }
   }
 
   // scratch sized by max_chunk (src/engine.mm:398-449)
@@ -385,8 +403,11 @@ static int open_engine(rl_engine *e, const char *path, int max_ctx, int max_chun
   for (const auto &kv : e->mats) {
     const QTensor &q = *kv.second.q;
     xs = std::max(xs, q.k);
-    if (q.kind != kKindF16b && !kv.second.moe_gate_up && kv.first.find(".moe.") == std::string::npos)
-      lin_ws = std::max(lin_ws, rlq_linear_workspace_bytes((int)std::min<size_t>(R, 16 * 1024), q.k, q.n_pad));
+    // every matrix rl_linear, rl_mlp or the head runs through the linear kernels, the MoE
+    // router included, at up to max_chunk rows (expert stacks run on the MoE workspace)
+    const bool expert_stack = ends_with(kv.first, ".moe.gate_up") || ends_with(kv.first, ".moe.down");
+    if (q.kind != kKindF16b && !expert_stack)
+      lin_ws = std::max(lin_ws, rlq_linear_workspace_bytes(max_chunk, q.k, q.n_pad));
   }
   e->x_stride = (xs + 7) / 8 * 8;
   for (int i = 0; i < c.layers; ++i)
@@ -418,6 +439,11 @@ static int open_engine(rl_engine *e, const char *path, int max_ctx, int max_chun
   const size_t chunks = (std::max<size_t>(e->logits.bytes / 4, 1) + kTopkChunk - 1) / kTopkChunk + 1;
   if (int rc = dev_alloc(e->topk_v, chunks * kTopkMaxK * 4, "top-k")) return rc;
   if (int rc = dev_alloc(e->topk_i, chunks * kTopkMaxK * 4, "top-k")) return rc;
+  // the second merge buffer: the groups of the first merge pass, k best each (later passes
+  // shrink and alternate between the two)
+  const size_t groups = (chunks * kTopkMaxK + kTopkMergeGroup - 1) / kTopkMergeGroup;
+  if (int rc = dev_alloc(e->topk_v2, groups * kTopkMaxK * 4, "top-k")) return rc;
+  if (int rc = dev_alloc(e->topk_i2, groups * kTopkMaxK * 4, "top-k")) return rc;
   if (int rc = dev_alloc(e->topk_out_v, kTopkMaxK * 4, "top-k")) return rc;
   if (int rc = dev_alloc(e->topk_out_i, kTopkMaxK * 4, "top-k")) return rc;
   return 0;
@@ -452,6 +478,14 @@ static int linear_rows(rl_engine *e, const EngineTensor &t, int r0, int N, const
                        e->linear_ws.p, e->linear_ws.bytes, st);
 }
 
+static int norm_with(rl_engine *e, const float *w, const float *h, int h_stride, int rows, _Float16 *xn,
+                     int xn_stride, hipStream_t st) {
+  const ModelConfig &c = e->model->config();
+  rms_norm_kernel<<<rows, kNormThreads, 0, st>>>(h, h_stride, w, c.hidden, c.norm_eps, xn, xn_stride);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
 static int norm_rows(rl_engine *e, int which, int layer, const float *h, int h_stride, int rows, _Float16 *xn,
                      int xn_stride, hipStream_t st) {
   const ModelConfig &c = e->model->config();
@@ -468,9 +502,7 @@ static int norm_rows(rl_engine *e, int which, int layer, const float *h, int h_s
     w = it == e->floats.end() ? nullptr : it->second.as<float>();
   }
   RLQ_REQUIRE(w, "model has no float tensor for norm %d of layer %d", which, layer);
-  rms_norm_kernel<<<rows, kNormThreads, 0, st>>>(h, h_stride, w, c.hidden, c.norm_eps, xn, xn_stride);
-  RLQ_HIP(hipGetLastError());
-  return 0;
+  return norm_with(e, w, h, h_stride, rows, xn, xn_stride, st);
 }
 
 static int top_k_device(rl_engine *e, const float *x, int n, int k, int32_t *ids, float *vals, hipStream_t st) {
@@ -482,18 +514,26 @@ static int top_k_device(rl_engine *e, const float *x, int n, int k, int32_t *ids
   RLQ_REQUIRE((size_t)chunks * k * 4 <= e->topk_v.bytes, "rl_top_k_device: n=%d is more than the engine's logits", n);
   topk_chunk_kernel<<<chunks, kTopkThreads, 0, st>>>(x, n, k, e->topk_v.as<float>(), e->topk_i.as<int>());
   RLQ_HIP(hipGetLastError());
-  const int m = chunks * k, per = (m + kTopkMergeThreads - 1) / kTopkMergeThreads;
-#define RLQ_TOPK_MERGE(P)                                                                                       \
-  topk_merge_kernel<P><<<1, kTopkMergeThreads, 0, st>>>(e->topk_v.as<float>(), e->topk_i.as<int>(), m, k,       \
-                                                        e->topk_out_v.as<float>(), e->topk_out_i.as<int>())
-  if (per <= 1) RLQ_TOPK_MERGE(1);
-  else if (per <= 4) RLQ_TOPK_MERGE(4);
-  else if (per <= 16) RLQ_TOPK_MERGE(16);
-  else if (per <= 32) RLQ_TOPK_MERGE(32);
-  else if (per <= 64) RLQ_TOPK_MERGE(64);
-  else return fail("rl_top_k_device: %d candidates is more than one merge takes", m);
-#undef RLQ_TOPK_MERGE
-  RLQ_HIP(hipGetLastError());
+  // merge passes: ping-pong between the two candidate buffers until one group is left,
+  // which writes the result
+  float *cv = e->topk_v.as<float>(), *tv = e->topk_v2.as<float>();
+  int *ci = e->topk_i.as<int>(), *ti = e->topk_i2.as<int>();
+  for (int m = chunks * k;;) {
+    const int groups = (m + kTopkMergeGroup - 1) / kTopkMergeGroup;
+    float *ov = groups == 1 ? e->topk_out_v.as<float>() : tv;
+    int *oi = groups == 1 ? e->topk_out_i.as<int>() : ti;
+    RLQ_REQUIRE((size_t)groups * k * 4 <= (groups == 1 ? e->topk_out_v.bytes : e->topk_v2.bytes),
+                "rl_top_k_device: %d candidates do not fit the merge buffer", m);
+    const int per = (m + kTopkMergeThreads - 1) / kTopkMergeThreads;
+    if (per <= 1) topk_merge_kernel<1><<<groups, kTopkMergeThreads, 0, st>>>(cv, ci, m, k, ov, oi);
+    else if (per <= 4) topk_merge_kernel<4><<<groups, kTopkMergeThreads, 0, st>>>(cv, ci, m, k, ov, oi);
+    else topk_merge_kernel<kTopkMergePer><<<groups, kTopkMergeThreads, 0, st>>>(cv, ci, m, k, ov, oi);
+    RLQ_HIP(hipGetLastError());
+    if (groups == 1) break;
+    m = groups * k;
+    std::swap(cv, tv);
+    std::swap(ci, ti);
+  }
   std::vector<float> v(k);
   std::vector<int> i(k);
   RLQ_HIP(hipMemcpyAsync(v.data(), e->topk_out_v.p, (size_t)k * 4, hipMemcpyDeviceToHost, st));
@@ -619,6 +659,7 @@ const float *rl_head(rl_engine *e, const float *h, int h_stride, int rows, void 
   const int np = head->q->n_pad;
   if (linear_rows(e, *head, 0, np, xn, e->x_stride, rows, e->logits.as<float>(), np, 0, st)) return nullptr;
   e->head_rows_done = rows;
+  e->head_stream = st;
   return e->logits.as<float>();
 }
 
@@ -685,7 +726,18 @@ const float *rl_draft_head(rl_engine *e, const float *h_row, void *stream) {
   }
   auto st = static_cast<hipStream_t>(stream);
   _Float16 *xn = e->xn.as<_Float16>();
-  if (norm_rows(e, 2, 0, h_row, e->model->config().hidden, 1, xn, e->x_stride, st)) return nullptr;
+  const ModelConfig &c = e->model->config();
+  if (e->has_mtp) {
+    // a file with an MTP head: the draft row is normed with mtp.norm (src/engine.mm:1419-1424);
+    // a rotated file would rotate it instead, with a kernel that is not on this path
+    if (c.rot_block) {
+      fail("rl_draft_head: a rotated model file (rot_block %d) needs the rotation kernel, not built here", c.rot_block);
+      return nullptr;
+    }
+    if (norm_with(e, e->norm_mtp_out.as<float>(), h_row, c.hidden, 1, xn, e->x_stride, st)) return nullptr;
+  } else if (norm_rows(e, 2, 0, h_row, c.hidden, 1, xn, e->x_stride, st)) {
+    return nullptr;
+  }
   const int main_rows = rl_draft_main(e), tail = rl_draft_tail(e), np = head->q->n_pad;
   float *out = e->draft_logits.as<float>();
   if (linear_rows(e, *head, 0, main_rows, xn, e->x_stride, 1, out, np, 0, st)) return nullptr;
@@ -723,7 +775,8 @@ int rl_argmax(const rl_engine *e) {
   int32_t id = 0;
   float v;
   rl_engine *m = const_cast<rl_engine *>(e);   // the device top-k uses the engine's scratch
-  const int got = top_k_device(m, m->logits.as<float>(), e->model->config().vocab, 1, &id, &v, nullptr);
+  // on the stream of the rl_head that wrote the logits, so it runs after the head's kernels
+  const int got = top_k_device(m, m->logits.as<float>(), e->model->config().vocab, 1, &id, &v, e->head_stream);
   return got == 1 ? id : 0;
 }
 

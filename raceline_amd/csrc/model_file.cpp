@@ -2,6 +2,8 @@
 // defaults and fatal messages, over a read-only shared mapping of the file.
 #include "model_file.h"
 
+#include <climits>
+
 #include "json.h"
 #include "rlq_common.h"
 #include "../../include/rl_engine.h"
@@ -54,14 +56,17 @@ namespace {
 int get_int(const json::Value *obj, const char *key, int &out) {
   const json::Value *v = obj ? obj->get(key) : nullptr;
   if (!v || !v->is_number()) return fail("model header: missing integer '%s'", key);
-  out = v->integral ? (int)v->i64 : (int)v->num;
+  const double x = v->integral ? (double)v->i64 : v->num;
+  if (!(x >= INT_MIN && x <= INT_MAX)) return fail("model header: integer '%s' is out of range", key);
+  out = (int)x;
   return 0;
 }
 
 int get_int_or(const json::Value *obj, const char *key, int fallback) {
   const json::Value *v = obj ? obj->get(key) : nullptr;
   if (!v || !v->is_number()) return fallback;
-  return v->integral ? (int)v->i64 : (int)v->num;
+  const double x = v->integral ? (double)v->i64 : v->num;
+  return x >= INT_MIN && x <= INT_MAX ? (int)x : fallback;
 }
 
 double get_num_or(const json::Value *obj, const char *key, double fallback) {
@@ -203,11 +208,17 @@ int ModelFile::parse(const std::string &path) {
       if (int rc = get_offset(&t, "offset", name, ft.offset)) return rc;
       const json::Value *shape = t.get("shape");
       if (!shape || !shape->is_array()) return fail("model header: tensor '%s' has no shape", name.c_str());
+      // each dimension a whole number in [0, INT_MAX], and 4 bytes times their product
+      // representable, before the product is used to check the tensor lies in the file
+      uint64_t count = 1;
       for (const json::Value &d : shape->arr) {
-        if (!d.is_number() || d.num < 0) return fail("model header: tensor '%s' has a bad shape", name.c_str());
-        ft.shape.push_back((int)d.num);
+        if (!d.is_number() || !d.integral || d.i64 < 0 || d.i64 > INT_MAX)
+          return fail("model header: tensor '%s' has a bad shape", name.c_str());
+        ft.shape.push_back((int)d.i64);
+        if (__builtin_mul_overflow(count, (uint64_t)d.i64, &count) || count > (UINT64_MAX >> 2))
+          return fail("model header: tensor '%s' has a bad shape", name.c_str());
       }
-      if (int rc = in_file(name, ft.offset, 4 * (uint64_t)ft.count())) return rc;
+      if (int rc = in_file(name, ft.offset, 4 * count)) return rc;
       f_[name] = ft;
       continue;
     }

@@ -153,6 +153,57 @@ def write_moe_model(path, seed=0, native_book=None, hidden=256, experts=32, topk
     return m
 
 
+def _bf16_values(x):
+    """float32 values that bfloat16 holds exactly (the low 16 bits cleared)."""
+    return (np.ascontiguousarray(x, np.float32).view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+
+
+def write_head_model(path, hidden, vocab, native_book=None, seed=0, mtp=False):
+    """Only what the output head reads, at a real vocabulary: one layer of norms, final_norm
+    and lm_head [vocab][hidden]. The head is drawn directly as codes (uniform 0..15) with
+    bf16 scales and biases (affine) or row and column scales (native), not quantized from
+    floats, so that a 248,320-row head is written in seconds. mtp (native files) adds the
+    MTP head's mtp.fc [hidden][2 hidden] and mtp.norm, which make the engine norm a draft
+    row with mtp.norm (src/engine.mm:398,534)."""
+    rng = np.random.default_rng(seed)
+    cfg = config(hidden, 1, 512, vocab)
+    m = Model(path, cfg, native_book)
+    w = rlm.Writer(path)
+    w.begin("layer.0")
+    for name in ("layers.0.in_norm", "layers.0.post_norm"):
+        arr = rng.uniform(0.5, 1.5, hidden).astype(np.float32)
+        w.add_float(name, arr)
+        m.floats[name] = arr
+    w.end()
+    w.begin("head")
+    fin = rng.uniform(0.5, 1.5, hidden).astype(np.float32)
+    w.add_float("final_norm", fin)
+    m.floats["final_norm"] = fin
+    q = rng.integers(0, 16, size=(vocab, hidden), dtype=np.uint8)
+    if native_book:
+        s = rng.uniform(0.002, 0.02, vocab).astype(np.float32)
+        c = rng.uniform(0.5, 2.0, hidden).astype(np.float32)
+        w.add_native("lm_head", [("out", vocab)], q, s, c, native_book)
+        m.native["lm_head"] = (q, s, c, {"out": (0, vocab)})
+    else:
+        G = hidden // 64
+        sf = _bf16_values(rng.uniform(0.001, 0.006, (vocab, G)))
+        bf = _bf16_values(-7.5 * sf + rng.uniform(-0.002, 0.002, (vocab, G)))
+        w.add_blocked("lm_head", [("out", (q, sf, bf))])
+        m.affine["lm_head"] = (q, O.f32_to_bf16_bits(sf), O.f32_to_bf16_bits(bf), {"out": (0, vocab)})
+    if mtp:
+        assert native_book, "the reference's MTP head is in native files"
+        codes, s, c = native(rng, hidden, 2 * hidden, native_book)
+        w.add_native("mtp.fc", [("out", hidden)], codes, s, c, native_book)
+        m.native["mtp.fc"] = (codes, s, c, {"out": (0, hidden)})
+        mn = rng.uniform(0.5, 1.5, hidden).astype(np.float32)
+        w.add_float("mtp.norm", mn)
+        m.floats["mtp.norm"] = mn
+    w.end()
+    w.finish(rlm.native_meta(cfg, native_book) if native_book else rlm.affine_meta(cfg))
+    return m
+
+
 def linear_f64(m: Model, name: str, x, rows=None):
     """The oracle's product of the model's tensor `name` (rows [r0, r1) if given) with x
     (fp16 rows; for native tensors x already carries the column scale)."""

@@ -1,6 +1,7 @@
 """The .rlm writer (raceline_amd/rlm.py) and the library's reader (csrc/model_file.cpp),
-without a GPU: layout replay (the writer's placement recomputed by Layout, as
-tests/test_runtime.py:296-323 checks it for tools/convert.py), the blocked packing against
+without a GPU: the writer's bytes against the reference writer's (a golden sha256 made
+from tools/convert.py), layout replay (the writer's placement recomputed by Layout, the
+property tests/test_runtime.py:296-323 checks for tools/convert.py), the blocked packing against
 the oracle's restatement of tools/convert.py:92-117, the reader's tables against what the
 writer recorded, the reader's fatal cases (src/model_file.mm:44-167), rl_open's checks that
 run before any device work (src/engine.mm:394-396,516), rl_top_k's order
@@ -21,38 +22,68 @@ import oracle.engine as OE
 from raceline_amd import lib, rlm
 from raceline_amd.model import ModelFile, top_k
 from tests import model_files as MF
+from tests.golden import writer_case as WC
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def test_layout_replay_matches_the_writer(tmp_path):
-    """Replaying a conversion's calls on Layout gives the Writer's tables and end position."""
-    rng = np.random.default_rng(0)
-    w, plan = rlm.Writer(str(tmp_path / "t.rlm")), rlm.Layout()
-    for o in (w, plan):
-        o.begin("embed")
-        if o is w:
-            o.add_native_rows("embed", rng.integers(0, 16, (1000, 64), dtype=np.uint8), np.ones(1000, np.float32),
-                              np.ones(64, np.float32), "fp4")
+def _golden_files(w):
+    w.begin("files")
+    for name, data in WC.FILES.items():
+        w.add_file(name, data)
+    w.end()
+
+
+def test_writer_matches_the_reference_writer(tmp_path):
+    """rlm.Writer writes, byte for byte, the file tools/convert.py's Writer writes for the same
+    calls: every tensor kind, parts, an embedded file section and the header (the length and
+    sha256 that tests/golden/make_writer_golden.py recorded from the reference's writer)."""
+    import hashlib
+
+    golden = json.load(open(os.path.join(ROOT, "tests", "golden", "writer_golden.json")))
+    path = str(tmp_path / "golden.rlm")
+    WC.write(rlm.Writer(path), _golden_files)
+    data = open(path, "rb").read()
+    assert len(data) == golden["bytes"]
+    assert hashlib.sha256(data).hexdigest() == golden["sha256"]
+
+
+def test_layout_counts_what_the_writer_writes(tmp_path):
+    """Layout, given a Writer's sequence of calls (native matrices by their sizes only),
+    arrives at the Writer's section and tensor tables and its final offset, which is the
+    length of the finished file's body."""
+    rng = np.random.default_rng(23)
+    k = 256
+    gate, up = MF.affine_bf16(rng, 200, k), MF.affine_bf16(rng, 56, k)
+    rows_q = MF.affine_bf16(rng, 90, 128)
+    lm = MF.native(rng, 520, k, "int15")
+    tok = MF.native(rng, 33, 64, "fp4")
+    wr, lay = rlm.Writer(str(tmp_path / "w.rlm")), rlm.Layout()
+    for o in (wr, lay):
+        o.begin("tables")
+        o.add_rows("tok_affine", *rows_q[:3])
+        if o is wr:
+            o.add_native_rows("tok_native", *tok, "fp4")
         else:
-            o.add_native_rows_layout("embed", 1000, 64, "fp4")
+            o.add_native_rows_layout("tok_native", 33, 64, "fp4")
         o.end()
-        for i in range(3):
-            o.begin(f"layer.{i}")
-            o.add_float(f"layers.{i}.in_norm", np.ones(64, np.float32))
-            o.add_float(f"layers.{i}.lin.conv", np.ones((96, 4), np.float32))
-            parts = [("q", 300), ("k", 77), ("v", 123)]
-            if o is w:
-                o.add_native(f"layers.{i}.attn.qkv", parts, rng.integers(0, 16, (500, 64), dtype=np.uint8),
-                             np.ones(500, np.float32), np.ones(64, np.float32), "fp4")
-            else:
-                o.add_native_layout(f"layers.{i}.attn.qkv", parts, 64, "fp4")
-            o.add_dense(f"layers.{i}.moe.router", np.ones((33, 64), np.float16))
+        for i in range(2):
+            o.begin(f"blk.{i}")
+            o.add_blocked(f"blk.{i}.ffn", [("gate", gate[:3]), ("up", up[:3])])
+            o.add_float(f"blk.{i}.scale", np.full((3, 5), i, np.float32))
+            o.add_dense(f"blk.{i}.gate", np.zeros((260, 64), np.float16))
             o.end()
-    assert w.tensors == plan.tensors
-    assert w.sections == plan.sections
-    assert w.f.tell() == plan.pos
-    w.finish({})
+        o.begin("out")
+        if o is wr:
+            o.add_native("head", [("a", 500), ("b", 20)], *lm, "int15")
+        else:
+            o.add_native_layout("head", [("a", 500), ("b", 20)], k, "int15")
+        o.end()
+    assert wr.tensors == lay.tensors
+    assert wr.sections == lay.sections
+    assert wr.f.tell() == lay.pos
+    wr.finish({})
+    assert os.path.getsize(str(tmp_path / "w.rlm")) == lay.pos
 
 
 def test_blocked_packing_matches_the_oracle():
@@ -180,6 +211,15 @@ def test_reader_fatal_cases(tmp_path):
     bad = json.loads(json.dumps(h))
     del bad["quant"]["group"]
     _fails(_rewrite(good, tmp_path / "group.rlm", bad), "missing integer 'group'")
+    # float tensor shapes: whole numbers within int range, whose byte count cannot wrap
+    f32 = next(n for n, t in h["tensors"].items() if t["kind"] == "f32")
+    for i, shape in enumerate(([1 << 31], [2.5], [1 << 20, 1 << 20, 1 << 20, 1 << 10], [-3])):
+        bad = json.loads(json.dumps(h))
+        bad["tensors"][f32]["shape"] = shape
+        _fails(_rewrite(good, tmp_path / f"shape{i}.rlm", bad), f"tensor '{f32}' has a bad shape")
+    bad = json.loads(json.dumps(h))
+    bad["config"]["hidden_size"] = 1 << 40
+    _fails(_rewrite(good, tmp_path / "bigint.rlm", bad), "integer 'hidden_size' is out of range")
     with ModelFile(good) as f:
         with pytest.raises(lib.RlqError, match="model has no tensor 'layers.9.mlp.down'"):
             f.tensor("layers.9.mlp.down")

@@ -155,13 +155,19 @@ class _Placement:
 
     def add_blocked(self, name, named_parts):
         """Affine matrices stacked as one q4a tensor: named_parts = [(part name, (q, s, b))]."""
-        w, s, b, n_pad, spans = pack_blocked([p for _, p in named_parts])
-        entry = {"kind": "q4a", "section": self._section(), "k": int(named_parts[0][1][0].shape[1]),
-                 "n": sum(r for _, r in spans), "n_pad": n_pad}
+        self.add_blocked_packed(name, [pn for pn, _ in named_parts], pack_blocked([p for _, p in named_parts]))
+
+    def add_blocked_packed(self, name, part_names, packed):
+        """A q4a tensor from what pack_blocked returned, (w, s, b, n_pad, spans), with the
+        parts' names: the same entry and bytes as add_blocked, without packing again (a
+        tensor written to several places or files is packed once)."""
+        w, s, b, n_pad, spans = packed
+        entry = {"kind": "q4a", "section": self._section(), "k": int(w.shape[1]), "n": sum(r for _, r in spans),
+                 "n_pad": n_pad}
         entry["w"] = self.blob(w)
         entry["s"] = self.blob(s)
         entry["b"] = self.blob(b)
-        entry["parts"] = {pn: {"offset": o, "n": r} for (pn, _), (o, r) in zip(named_parts, spans)}
+        entry["parts"] = {pn: {"offset": o, "n": r} for pn, (o, r) in zip(part_names, spans)}
         self.tensors[name] = entry
 
     def add_native(self, name, named_parts, codes, s, c, book):
@@ -262,14 +268,15 @@ class Writer(_Placement):
         hdr = json.dumps(dict(meta, sections=self.sections, tensors=self.tensors, files=self.files),
                          separators=(",", ":")).encode()
         if 16 + len(hdr) > self.header_room:
-            raise ValueError(f"header ({16 + len(hdr)} bytes) does not fit the reserved {self.header_room}")
+            raise ValueError(f"the {16 + len(hdr)}-byte header is larger than the {self.header_room} bytes kept "
+                             f"for it at the start of the file")
         self.f.seek(0)
         self.f.write(MAGIC + struct.pack("<IQ", VERSION, len(hdr)) + hdr)
         self.f.close()
 
 
 class Layout(_Placement):
-    """Where a Writer puts things, computed without writing anything."""
+    """The placement a Writer makes for the same calls, counted only: no bytes are written."""
 
     def __init__(self):
         self.header_room = HEADER_PAGES * PAGE

@@ -99,12 +99,15 @@ def expert_rows(e: int, rows_per_expert: int):
 
 
 def moe_layer_f64(x, logits, gu, dn, E: int, topk: int, I: int, H: int, norm_topk: bool = True,
-                  scale_dtype: str = "f16", h0=None, act_f16: bool = True):
+                  scale_dtype: str = "f16", h0=None, act_f16: bool = True, acts=None):
     """The whole MoE MLP of src/engine.mm:965-1059 on the CPU, float64 throughout
     except the SwiGLU output, which the reference stores as half (ops.metal:454).
 
     x: [T][H] fp16 (the normed rows); logits [T][E+1] float32;
     gu = (q [(E+1)*2I][H], s, b), dn = (q [(E+1)*H][I], s, b) with 16-bit scale bits.
+    acts: optional fp16 activations [T*S][I] in (token, slot) order used in place of the
+    SwiGLU of the gate/up product (a test passes the kernel's own, so that the check of the
+    down product and the combine does not depend on where a half rounds).
     Returns (h [T][H] float64 = h0 + sum over slots of w * expert(x), sel, w)."""
     x = np.asarray(x)
     T = x.shape[0]
@@ -118,8 +121,11 @@ def moe_layer_f64(x, logits, gu, dn, E: int, topk: int, I: int, H: int, norm_top
             e = int(sel[t * S + s])
             rg = expert_rows(e, 2 * I)
             rd = expert_rows(e, H)
-            g = linear_affine_f64(x[t:t + 1].astype(np.float64), qg[rg], sg[rg], bg[rg], scale_dtype)
-            a = swiglu_f16(g, I) if act_f16 else (silu(g[:, :I]) * g[:, I:])
+            if acts is not None:
+                a = np.asarray(acts[t * S + s:t * S + s + 1], np.float16)
+            else:
+                g = linear_affine_f64(x[t:t + 1].astype(np.float64), qg[rg], sg[rg], bg[rg], scale_dtype)
+                a = swiglu_f16(g, I) if act_f16 else (silu(g[:, :I]) * g[:, I:])
             y = linear_affine_f64(np.asarray(a, np.float64), qd[rd], sd[rd], bd[rd], scale_dtype)
             h[t] += w[t * S + s] * y[0]
     return h, sel, w
@@ -155,15 +161,15 @@ def moe_linear_native_f64(a, items, n_items: int, slots, codes, s_row, Ne: int, 
 
 
 def moe_layer_native_f64(x, logits, gu, dn, cs, slots, E: int, topk: int, I: int, H: int, book: str,
-                         norm_topk: bool = True, h0=None):
+                         norm_topk: bool = True, h0=None, acts=None):
     """The native MoE MLP of src/engine.mm:965-1059 (route, gather, linear_q4n_moe,
     swiglu with the down matrix's column scale, linear_q4n_moe, combine), token by token
     in float64 except the SwiGLU output, stored as half (ops.metal:454).
 
     x: [T][H] fp16 (already times gate_up's column scale, as the reference folds it);
     gu = (codes [n_slots*2I][H], s [n_slots*2I]): gate rows then up rows per slot;
-    dn = (codes [n_slots*H][I], s [n_slots*H]); cs [I] or None; slots [E+1].
-    Returns (h [T][H] float64, sel, w)."""
+    dn = (codes [n_slots*H][I], s [n_slots*H]); cs [I] or None; slots [E+1]; acts as in
+    moe_layer_f64. Returns (h [T][H] float64, sel, w)."""
     x = np.asarray(x)
     T = x.shape[0]
     S = topk + 1
@@ -173,8 +179,11 @@ def moe_layer_native_f64(x, logits, gu, dn, cs, slots, E: int, topk: int, I: int
     for t in range(T):
         for j in range(S):
             slot = int(slots[int(sel[t * S + j])])
-            g = linear_native_f64(x[t:t + 1], qg[expert_rows(slot, 2 * I)], sg[expert_rows(slot, 2 * I)], book)
-            a = swiglu_f16(g, I, cs)
+            if acts is not None:
+                a = np.asarray(acts[t * S + j:t * S + j + 1], np.float16)
+            else:
+                g = linear_native_f64(x[t:t + 1], qg[expert_rows(slot, 2 * I)], sg[expert_rows(slot, 2 * I)], book)
+                a = swiglu_f16(g, I, cs)
             y = linear_native_f64(a, qd[expert_rows(slot, H)], sd[expert_rows(slot, H)], book)
             h[t] += w[t * S + j] * y[0]
     return h, sel, w

@@ -10,6 +10,10 @@ writer, against the oracle:
   :965-1059; native and affine stacks): the MLP's contribution within 1e-3; a token's
   result is the same bits whatever other tokens share the call, within one kernel family
   (the decode kernel up to 8 rows, the prefill kernel above; the MoE kernels throughout).
+  At the other model sizes the contribution is held to 1e-3 once the oracle's down product
+  takes the GPU's own half activations, and to a looser bound against the oracle's own.
+- Chunking (ops.metal:60-72): a row from an 8-row call (decode kernel) and from a 9-row
+  call (prefill kernel) agree within a stated bound, for rl_linear and rl_mlp.
 - rl_head and the draft head (engine.mm:1425-1458,1634-1638): logits within 1e-3; the draft
   logits are exactly the main and tail slices of the full head's; rl_top_k_device and
   rl_argmax give rl_top_k's ids and values exactly.
@@ -247,6 +251,132 @@ def test_moe_layer_other_sizes(gpu, tmp_path, book):
             _sync()
             ref = _moe_ref(m, 0, h0)
             _check_layer(h.cpu().numpy().astype(np.float64) - h0, ref - h0, f"MoE T={T} book={book}")
+
+
+def _dense_from_gpu_acts(e, m, layer, h0, gpu):
+    """The dense MLP's contribution computed by the oracle's down product from the GPU's own
+    half activations. rl_norm, rl_linear on the gate/up matrix and the SwiGLU kernel are the
+    steps rl_mlp runs (the same kernels on the same rows, so the same bits)."""
+    from raceline_amd import ops
+
+    I = m.cfg["intermediate_size"]
+    xn = e.norm(1, layer, to_dev(h0, gpu))
+    g = e.linear(f"layers.{layer}.mlp.gate_up", xn, n=2 * I)
+    cs = _col_scale(m, f"layers.{layer}.mlp.down")
+    act = ops.moe_swiglu(g, I, None if cs is None else to_dev(cs, gpu))
+    _sync()
+    return MF.linear_f64(m, f"layers.{layer}.mlp.down", act.cpu().numpy())
+
+
+def _moe_from_gpu_acts(e, m, layer, h0, gpu):
+    """The MoE MLP by the oracle (routing, down products, combine) from the GPU's normed rows,
+    router logits and half activations, taken by the step entry points that rlq_moe and
+    rlq_moe_native equal bit for bit (the gate/up product with the SwiGLU fused)."""
+    import torch
+
+    from raceline_amd import ops
+    from tests.qdata import upload_mlx
+
+    cfg = m.cfg
+    E, topk, I, H = cfg["num_experts"], cfg["num_experts_per_tok"], cfg["moe_intermediate_size"], cfg["hidden_size"]
+    gu, dn = f"layers.{layer}.moe.gate_up", f"layers.{layer}.moe.down"
+    xn = e.norm(1, layer, to_dev(h0, gpu))
+    logits = e.linear(f"layers.{layer}.moe.router", xn, n=E + 1)
+    r = ops.moe_route(logits, E, topk)
+    if m.book:
+        qg, sg, _, _ = m.native[gu]
+        stack = ops.pack_moe_native(to_dev(O.pack_nibbles_u32(qg).view(np.int32), gpu), to_dev(sg, gpu), 2 * I, m.book)
+        slots = torch.arange(E + 1, dtype=torch.int32, device=gpu)
+        act = ops.moe_gate_up_native(xn, stack, slots, r, to_dev(m.native[dn][2], gpu))
+    else:
+        mw = ops.pack_moe(upload_mlx(*m.affine[gu][:3], "bf16", gpu), upload_mlx(*m.affine[dn][:3], "bf16", gpu),
+                          E, H, I)
+        act = ops.moe_gate_up(xn, mw, r)
+    acts = act[r.inv.long()]                      # (token, slot) order
+    _sync()
+    xn_h, lg, acts_h = xn.cpu().numpy(), logits.cpu().numpy(), acts.cpu().numpy()
+    if m.book:
+        (qg, sg, _, _), (qd, sd, cd, _) = m.native[gu], m.native[dn]
+        ref, _, _ = O.moe_layer_native_f64(xn_h, lg, (qg, sg), (qd, sd), cd, np.arange(E + 1), E, topk, I, H, m.book,
+                                           h0=h0, acts=acts_h)
+    else:
+        ref, _, _ = O.moe_layer_f64(xn_h, lg, m.affine[gu][:3], m.affine[dn][:3], E, topk, I, H, scale_dtype="bf16",
+                                    h0=h0, acts=acts_h)
+    return ref
+
+
+@pytest.mark.parametrize("book", [None, "int15"])
+@pytest.mark.parametrize("hidden,inter", [(320, 768), (512, 256)])
+def test_dense_mlp_other_sizes_from_the_gpus_activations(gpu, tmp_path, book, hidden, inter):
+    """rl_mlp at the other sizes, held to 1e-3 of the fp64 product once the oracle's down
+    product takes the GPU's own half activations (where a half rounds is then the same on
+    both sides; the gate/up product and the SwiGLU are checked by the other tests)."""
+    m = MF.write_dense_model(str(tmp_path / "m.rlm"), seed=hidden + inter + 1, native_book=book, hidden=hidden,
+                             intermediate=inter, vocab=700, layers=1)
+    with Engine(m.path, max_chunk=64) as e:
+        for T in (1, 7, 33):
+            h0 = np.random.default_rng(T + hidden + 1).standard_normal((T, hidden)).astype(np.float32)
+            h = to_dev(h0, gpu)
+            e.mlp(0, h)
+            _sync()
+            ref = _dense_from_gpu_acts(e, m, 0, h0, gpu)
+            O.check_close(h.cpu().numpy().astype(np.float64) - h0, ref, TOL,
+                          f"dense MLP T={T} H={hidden} I={inter} book={book}")
+
+
+@pytest.mark.parametrize("book", [None, "fp4", "int15"])
+def test_moe_other_sizes_from_the_gpus_activations(gpu, tmp_path, book):
+    """rl_mlp over a mixture of experts of other sizes (H = 512, 32 experts + shared, top-3,
+    I = 384), held to 1e-3 of the oracle fed the GPU's own activations."""
+    m = MF.write_moe_model(str(tmp_path / "moe.rlm"), seed=22, native_book=book, hidden=512, experts=32, topk=3,
+                           moe_inter=384)
+    with Engine(m.path, max_chunk=64) as e:
+        for T in (1, 5, 40):
+            h0 = np.random.default_rng(310 + T).standard_normal((T, 512)).astype(np.float32)
+            h = to_dev(h0, gpu)
+            e.mlp(0, h)
+            _sync()
+            ref = _moe_from_gpu_acts(e, m, 0, h0, gpu)
+            O.check_close(h.cpu().numpy().astype(np.float64) - h0, ref - h0, TOL, f"MoE T={T} book={book}")
+
+
+CHUNK_LINEAR_BOUND = 5e-5     # max |row from 8 rows - row from 9 rows| / rms
+CHUNK_MLP_BULK, CHUNK_MLP_MAX = 2e-4, 3e-3
+
+
+@pytest.mark.parametrize("book", BOOKS)
+def test_rows_agree_between_decode_and_prefill_chunks(gpu, tmp_path, book):
+    """The reference gives a token the same bits however a prompt is chunked
+    (kernels/ops.metal:60-72). Here a call of up to 8 rows runs the decode kernel and a longer
+    one the prefill kernel, which sum in different orders, so a row from an 8-row call and
+    from a 9-row call are held to a bound instead: rl_linear within CHUNK_LINEAR_BOUND of the
+    output's rms; rl_mlp, whose products pass through half activations that may round
+    either way, within CHUNK_MLP_BULK (rms) and CHUNK_MLP_MAX (max) of its contribution's rms."""
+    m = MF.write_dense_model(str(tmp_path / "m.rlm"), seed=40, native_book=book)
+    rng = np.random.default_rng(41)
+    with Engine(m.path, max_chunk=64) as e:
+        x = to_dev(rng.standard_normal((9, 512)).astype(np.float16), gpu)
+        for name, k, n in (("layers.0.attn.qkv", 256, 1024), ("layers.1.mlp.gate_up", 256, 1024),
+                           ("layers.0.mlp.down", 512, 256), ("lm_head", 256, 1000)):
+            y8 = e.linear(name, x[:8, :k].contiguous(), n=n)
+            y9 = e.linear(name, x[:9, :k].contiguous(), n=n)
+            _sync()
+            a, b = y8.cpu().numpy().astype(np.float64), y9.cpu().numpy()[:8].astype(np.float64)
+            rms = float(np.sqrt(np.mean(b ** 2)))
+            d = float(np.abs(a - b).max()) / rms
+            print(f"[chunk] {name} book={book}: max|y(8 rows) - y(9 rows)|/rms = {d:.2e}")
+            assert d <= CHUNK_LINEAR_BOUND, f"{name}: {d:.3e}"
+        h0 = rng.standard_normal((9, 256)).astype(np.float32)
+        h8, h9 = to_dev(h0[:8].copy(), gpu), to_dev(h0.copy(), gpu)
+        e.mlp(1, h8)
+        e.mlp(1, h9)
+        _sync()
+        a = h8.cpu().numpy().astype(np.float64) - h0[:8]
+        b = h9.cpu().numpy()[:8].astype(np.float64) - h0[:8]
+        rms = float(np.sqrt(np.mean(b ** 2)))
+        bulk, worst = float(np.sqrt(np.mean((a - b) ** 2))) / rms, float(np.abs(a - b).max()) / rms
+        print(f"[chunk] rl_mlp book={book}: rms {bulk:.2e}, max {worst:.2e} of the contribution's rms")
+        assert bulk <= CHUNK_MLP_BULK and worst <= CHUNK_MLP_MAX, f"rl_mlp: {bulk:.3e} {worst:.3e}"
 
 
 @pytest.mark.parametrize("book", BOOKS)

@@ -88,6 +88,34 @@ def test_moe_layer_linearity_in_h0_and_weights():
     np.testing.assert_allclose(h[t], acc, rtol=1e-9, atol=1e-12)
 
 
+def test_given_activations_replace_the_swiglu():
+    """acts: the layer's own half activations (in token, slot order) give its result bit for
+    bit, and a changed activation moves h by exactly w * (delta a) . W_down of that slot."""
+    rng = np.random.default_rng(24)
+    E, K, I, H, T = 8, 2, 64, 128, 2
+    gu = O.quantize_affine_rtn((rng.standard_normal(((E + 1) * 2 * I, H)) * 0.02).astype(np.float32))
+    dn = O.quantize_affine_rtn((rng.standard_normal(((E + 1) * H, I)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    logits = rng.standard_normal((T, E + 1)).astype(np.float32)
+    h, sel, w = O.moe_layer_f64(x, logits, gu, dn, E, K, I, H)
+    S = K + 1
+    acts = np.zeros((T * S, I), np.float16)
+    for a in range(T * S):
+        e = int(sel[a])
+        Wge = O.dequant_affine(*gu)[e * 2 * I:(e + 1) * 2 * I].astype(np.float64)
+        acts[a] = O.swiglu_f16(x[a // S:a // S + 1].astype(np.float64) @ Wge.T, I)[0]
+    h2, _, _ = O.moe_layer_f64(x, logits, gu, dn, E, K, I, H, acts=acts)
+    np.testing.assert_array_equal(h2, h)
+    bumped = acts.copy()
+    bumped[S + 1, 5] = np.float16(float(bumped[S + 1, 5]) + 0.25)
+    h3, _, _ = O.moe_layer_f64(x, logits, gu, dn, E, K, I, H, acts=bumped)
+    e = int(sel[S + 1])
+    Wde = O.dequant_affine(*dn)[e * H:(e + 1) * H].astype(np.float64)
+    delta = float(bumped[S + 1, 5]) - float(acts[S + 1, 5])
+    np.testing.assert_allclose(h3[1] - h[1], w[S + 1] * delta * Wde[:, 5], rtol=1e-9, atol=1e-15)
+    np.testing.assert_array_equal(h3[0], h[0])
+
+
 def _native_stack(rng, n_slots, Ne, K):
     codes = rng.integers(0, 16, size=(n_slots * Ne, K), dtype=np.uint8)
     s_row = rng.uniform(0.01, 0.03, size=n_slots * Ne).astype(np.float32)

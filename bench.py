@@ -10,14 +10,21 @@ attn.qkv tensor, one linear: src/engine.mm:1163-1167), so four launches of the d
 kernel (qkv, o, gate_up, down), 4-bit affine g64 with fp16 scales, weights
 N(0, 0.02) quantized on the device and activations fp16 N(0, 1). Every step uses the next
 of >= 1 GiB of distinct weight copies so that the 256 MB Infinity Cache cannot serve
-re-reads. Steps are replayed from HIP graphs (one per copy) so that host launch cost does
-not pace the GPU. value = algorithmic bytes of the step / measured time per step.
+re-reads. The steps are replayed from one HIP graph so that host launch cost does not pace
+the GPU. value = algorithmic bytes of the step / measured time per step.
 
 Also reported under "detail": the M=5 layer, the 27B layer at M=1 and M=8 (config 3), the
 27B prefill layer at M=2048 (config 4, TFLOP/s against the dense fp16 MFMA peak), the MoE
-layer at T=1 and T=512 (config 5), each projection's kernel time, and the CPU baseline: the reference's numpy dequant + fp32
-matmul (oracle.linear_affine_cpu_f32) on a bounded sample, timed on this host. The
-six-launch layer (q, k, v as separate matrices) is reported under detail too.
+layer at T=1 and T=512 (config 5), each projection's kernel time, the six-launch layer (q,
+k, v as separate matrices), the native int15 MoE and linear, the 9B layer and the 27B
+prefill with bf16 scales (the .rlm files' scale type), the output head at a vocabulary of
+248,320, the engine's rl_mlp over .rlm files (dense 9B-shaped and the MoE layer) beside the
+sum of its parts, and the CPU baseline: the reference's numpy dequant + fp32 matmul
+(oracle.linear_affine_cpu_f32) on a bounded sample, timed on this host.
+
+Timing: each entry captures one HIP graph of exactly --steps consecutive steps over its
+rotating weight copies, replays it untimed (at least --warmup steps, and its first replay),
+then times one replay with HIP events on the stream it runs on.
 """
 
 from __future__ import annotations
@@ -58,17 +65,45 @@ def copies_for(shapes):
     return max(2, -(-CACHE_DEFEAT_BYTES // per))
 
 
-class LayerRunner:
-    """Pre-built buffers and HIP graphs of the layer's projections: one graph per weight
-    copy (a single step) and one holding a step on every copy in turn. Graphs are
-    captured and replayed on one stream, which the timing events bracket."""
+class StepGraphs:
+    """Timing of an arbitrary step over rotating weight copies: step c runs steps_per_copy[c %
+    n]. Every step runs once eagerly on a side stream (each call is valid before it is
+    captured); time_steps then captures one HIP graph of exactly the timed number of
+    consecutive steps and replays it on that stream, which the timing events bracket."""
+
+    def __init__(self, steps_per_copy):
+        import torch
+
+        self.torch = torch
+        self.fns = list(steps_per_copy)
+        # The step's buffers come from the default stream's allocator pool, whose blocks may
+        # still be written by kernels queued there (weight generation, freed temporaries).
+        # The MoE step computes addresses from the routing tables it writes into such a
+        # block: without this wait a queued kernel can overwrite them under the side stream.
+        torch.cuda.synchronize()
+        self.stream = torch.cuda.Stream()
+        with torch.cuda.stream(self.stream):
+            for fn in self.fns:
+                fn()
+        torch.cuda.synchronize()
+
+    def graph_of(self, count):
+        """One graph of `count` consecutive steps, starting at copy 0."""
+        g = self.torch.cuda.CUDAGraph()
+        with self.torch.cuda.graph(g, stream=self.stream):
+            for i in range(count):
+                self.fns[i % len(self.fns)]()
+        return g
+
+
+class LayerRunner(StepGraphs):
+    """The layer's projections as one step: step c runs every projection on weight copy c."""
 
     def __init__(self, layers, shapes, M, device, kernel=0, outliers=0.0):
         import torch
 
         from raceline_amd import ops, synth
 
-        self.torch = torch
         self.layers, self.shapes, self.M = layers, shapes, M
         self.xs = {K: synth.random_activations(M, K, 7 + K, device, outliers) for _, K, _ in shapes}
         self.ys = [torch.empty((M, N), dtype=torch.float32, device=device) for _, _, N in shapes]
@@ -76,26 +111,7 @@ class LayerRunner:
         # grow the workspace to its largest size before capture (no allocation inside a graph)
         for (_, K, N) in shapes:
             ops._WS.get(device, ops.workspace_bytes(M, K, N))
-        # The buffers above come from the default stream's allocator pool, whose blocks may
-        # still be written by kernels queued there (weight generation, freed temporaries):
-        # the side stream starts only when that work is done.
-        torch.cuda.synchronize()
-        self.stream = torch.cuda.Stream()
-        with torch.cuda.stream(self.stream):
-            for c in range(len(layers)):
-                self.run_eager(c)          # every call is valid before it is captured
-        torch.cuda.synchronize()
-        self.step_graphs = []
-        for c in range(len(layers)):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=self.stream):
-                self.run_eager(c)
-            self.step_graphs.append(g)
-        self.round_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.round_graph, stream=self.stream):
-            for c in range(len(layers)):
-                self.run_eager(c)
-        torch.cuda.synchronize()
+        super().__init__([(lambda c=c: self.run_eager(c)) for c in range(len(layers))])
 
     def run_eager(self, c, only=None):
         from raceline_amd import ops
@@ -105,67 +121,60 @@ class LayerRunner:
                 continue
             ops.linear(self.xs[K], wt, out=self.ys[i], kernel=self.kernel)
 
-    def run_steps(self, first, count):
-        """Replays `count` steps starting at copy `first`: whole rounds from the round graph."""
-        n = len(self.step_graphs)
-        i = 0
-        while i < count:
-            if (first + i) % n == 0 and count - i >= n:
-                self.round_graph.replay()
-                i += n
-            else:
-                self.step_graphs[(first + i) % n].replay()
-                i += 1
-
 
 def time_steps(runner, steps, warmup):
+    """Seconds per step: one captured graph of exactly `steps` consecutive steps, replayed
+    max(1, ceil(warmup / steps)) times untimed (at least `warmup` steps, and the graph's first
+    replay, which costs more than later ones), then once between two events on its stream."""
     torch = runner.torch
+    g = runner.graph_of(steps)
     with torch.cuda.stream(runner.stream):
-        runner.run_steps(0, warmup)
+        for _ in range(max(1, -(-warmup // steps))):
+            g.replay()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        first = -(-warmup // len(runner.step_graphs)) * len(runner.step_graphs)  # start on a round boundary
         start.record()
-        runner.run_steps(first, steps)
+        g.replay()
         end.record()
         torch.cuda.synchronize()
+    del g
     return start.elapsed_time(end) / 1e3 / steps      # seconds per step
 
 
-class StepGraphs:
-    """HIP graphs of an arbitrary step: one graph per weight copy, captured and replayed on
-    one stream that the timing events bracket (same scheme as LayerRunner)."""
-
-    def __init__(self, steps_per_copy):
-        import torch
-
-        self.torch = torch
-        # The step's buffers come from the default stream's allocator pool, whose blocks may
-        # still be written by kernels queued there (weight generation, freed temporaries).
-        # The MoE step computes addresses from the routing tables it writes into such a
-        # block: without this wait a queued kernel can overwrite them under the side stream.
-        torch.cuda.synchronize()
-        self.stream = torch.cuda.Stream()
-        with torch.cuda.stream(self.stream):
-            for fn in steps_per_copy:
-                fn()
-        torch.cuda.synchronize()
-        self.step_graphs = []
-        for fn in steps_per_copy:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=self.stream):
-                fn()
-            self.step_graphs.append(g)
-        self.round_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.round_graph, stream=self.stream):
-            for fn in steps_per_copy:
-                fn()
-        torch.cuda.synchronize()
-
-    run_steps = LayerRunner.run_steps
-
-
 MOE_EXPERT_BYTES = 1769472   # codes + fp16 s/b of one expert's gate_up [1024][2048] and down [2048][512]
+MOE_T1_STEPS = 64            # distinct routings of the one-token MoE step
+
+
+def moe_step_logits(T, E, copies, device):
+    """Router logits for the MoE steps: one [T][E+1] matrix per step. A one-token step
+    reads only its 9 experts (16 MB), so the same routing on every step of a copy would
+    find them in the 256 MB Infinity Cache; at T = 1 each of MOE_T1_STEPS steps draws its
+    own logits, so a round of steps touches several hundred MB per copy. At T = 512 a step
+    reads every expert (more than the cache holds) and one routing serves every copy."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(601 + T)
+    n = max(MOE_T1_STEPS, copies) if T == 1 else copies
+    one = T > 1
+    mats = [torch.randn((T, E + 1), generator=g, device=device, dtype=torch.float32) for _ in range(1 if one else n)]
+    return [mats[0]] * n if one else mats
+
+
+def moe_distinct_experts(logits, E, topk):
+    """Distinct experts a step reads (its routed ones and the shared one), averaged over the
+    steps' routings."""
+    import torch
+
+    from raceline_amd import ops
+
+    seen = {}
+    for lg in logits:
+        key = id(lg)
+        if key not in seen:
+            seen[key] = int(torch.unique(ops.moe_route(lg, E, topk).sel).numel())
+    vals = [seen[id(lg)] for lg in logits]
+    return round(sum(vals) / len(vals), 2)
 
 
 def bench_moe(device, steps, warmup):
@@ -191,17 +200,16 @@ def bench_moe(device, steps, warmup):
     out = {}
     for T in MOE["tokens"]:
         x = synth.random_activations(T, H, 600 + T, device)
-        g = torch.Generator(device=device)
-        g.manual_seed(601 + T)
-        logits = torch.randn((T, E + 1), generator=g, device=device, dtype=torch.float32)
+        logits = moe_step_logits(T, E, copies, device)
         h = torch.zeros((T, H), dtype=torch.float32, device=device)
         ws = torch.empty(ops.moe_workspace_bytes(T, E, topk, H, I), dtype=torch.uint8, device=device)
-        fns = [(lambda mw=mw: ops.moe(x, logits, mw, topk, h, workspace=ws)) for mw in mws]
+        fns = [(lambda mw=mws[j % copies], lg=lg: ops.moe(x, lg, mw, topk, h, workspace=ws))
+               for j, lg in enumerate(logits)]
         sg = StepGraphs(fns)
         t = time_steps(sg, steps, warmup)
-        distinct = int(torch.unique(ops.moe_route(logits, E, topk).sel).numel())
+        distinct = moe_distinct_experts(logits, E, topk)
         A = T * (topk + 1)
-        nbytes = distinct * MOE_EXPERT_BYTES + A * (2 * H * 2 + 2 * I * 4 + I * 2 + H * 4)
+        nbytes = int(round(distinct * MOE_EXPERT_BYTES)) + A * (2 * H * 2 + 2 * I * 4 + I * 2 + H * 4)
         flops = 2 * A * 3 * H * I
         out[f"moe_t{T}"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
                             "TFLOP/s": round(flops / t / 1e12, 2), "distinct_experts": distinct,
@@ -250,15 +258,17 @@ def bench_moe_native(device, steps, warmup):
     out = {}
     for T in MOE["tokens"]:
         x = synth.random_activations(T, H, 600 + T, device)
-        g.manual_seed(601 + T)
-        logits = torch.randn((T, E + 1), generator=g, device=device, dtype=torch.float32)
+        logits = moe_step_logits(T, E, copies, device)
         h = torch.zeros((T, H), dtype=torch.float32, device=device)
-        fns = [(lambda gu=gu, dn=dn: ops.moe_native(x, logits, gu, dn, slots, topk, h, cs=cs)) for gu, dn in stacks]
+        ws = torch.empty(ops.moe_workspace_bytes(T, E, topk, H, I), dtype=torch.uint8, device=device)
+        fns = [(lambda st=stacks[j % copies], lg=lg: ops.moe_native(x, lg, st[0], st[1], slots, topk, h, cs=cs,
+                                                                     workspace=ws))
+               for j, lg in enumerate(logits)]
         sg = StepGraphs(fns)
         t = time_steps(sg, steps, warmup)
-        distinct = int(torch.unique(ops.moe_route(logits, E, topk).sel).numel())
+        distinct = moe_distinct_experts(logits, E, topk)
         A = T * (topk + 1)
-        nbytes = distinct * NATIVE_EXPERT_BYTES + A * (2 * H + 2 * I * 2 + 2 * H * 4)
+        nbytes = int(round(distinct * NATIVE_EXPERT_BYTES)) + A * (2 * H + 2 * I * 2 + 2 * H * 4)
         out[f"moe_native_t{T}"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
                                    "distinct_experts": distinct, "algorithmic_bytes": nbytes, "book": "int15"}
         log(f"[bench] native MoE T={T}: {t * 1e6:.1f} us/step, {nbytes / t / 1e9:.0f} GB/s ({distinct} experts)")
@@ -303,6 +313,169 @@ def bench_native_epilogue(device, steps, warmup):
         del nws
         torch.cuda.empty_cache()
     return {"native_epilogue": out}
+
+
+HEAD_VOCAB = 248320           # the reference's Qwen3.5 vocabulary (tests/tiny_moe.py:121)
+
+
+def bench_bf16(device, steps, warmup):
+    """What real files run: tools/convert.py stores the affine scales and biases as bf16
+    (:73-79,189-195). The 9B decode layer at M = 1 (the headline's shapes) and the 27B
+    prefill layer at M = 2048 with bf16 scales and biases, timed as their fp16 entries."""
+    import torch
+
+    from raceline_amd.configs import CFG2_9B_STACKED, CFG3_27B, CFG4_PREFILL_M, linear_flops
+
+    out = {}
+    L9 = CFG2_9B_STACKED
+    l9 = build_layer_copies(L9, copies_for(L9), 1, device, torch.bfloat16)
+    r = LayerRunner(l9, L9, 1, device)
+    t = time_steps(r, steps, warmup)
+    out["layer_9b_m1_bf16"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(layer_bytes(L9, 1) / t / 1e9, 1)}
+    log(f"[bench] 9B layer M=1, bf16 scales: {t * 1e6:.1f} us/step")
+    del r, l9
+    torch.cuda.empty_cache()
+    l27 = build_layer_copies(CFG3_27B, 2, 2, device, torch.bfloat16)
+    rp = LayerRunner(l27, CFG3_27B, CFG4_PREFILL_M, device, outliers=0.01)
+    tp = time_steps(rp, max(4, steps // 5), 2)
+    flops = sum(linear_flops(CFG4_PREFILL_M, K, N) for _, K, N in CFG3_27B)
+    out["prefill_27b_m2048_bf16"] = {"us_per_step": round(tp * 1e6, 1), "TFLOP/s": round(flops / tp / 1e12, 1),
+                                     "frac_of_mfma_peak": round(flops / tp / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+    log(f"[bench] 27B prefill, bf16 scales: {flops / tp / 1e12:.1f} TFLOP/s")
+    del rp, l27
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_head(device, steps, warmup):
+    """The output head at the reference's vocabulary (src/engine.mm:1634-1638): 248,320 rows
+    of hidden 4096 and 5120, affine with bf16 scales (the .rlm format), one token (M = 1)
+    and a token with 4 drafts (M = 5), over >= 1 GiB of rotating copies; the largest single
+    matrix of a decode pass, HBM-bound like the decode layer."""
+    import torch
+
+    from raceline_amd.configs import linear_bytes
+
+    out = {}
+    for H in (4096, 5120):
+        shapes = [("lm_head", H, HEAD_VOCAB)]
+        copies = copies_for(shapes)
+        heads = build_layer_copies(shapes, copies, 30 + H, device, torch.bfloat16)
+        for M in (1, 5):
+            r = LayerRunner(heads, shapes, M, device)
+            t = time_steps(r, steps, warmup)
+            nb = linear_bytes(M, H, HEAD_VOCAB)
+            out[f"head_248k_h{H}_m{M}"] = {"us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
+                                           "frac_of_hbm_peak": round(nb / t / 1e9 / HBM_PEAK_GBS, 4),
+                                           "algorithmic_bytes": nb}
+            log(f"[bench] head 248320 x {H} M={M}: {t * 1e6:.1f} us, {nb / t / 1e9:.0f} GB/s")
+            del r
+        del heads
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_engine(device, steps, warmup, tmpdir):
+    """The engine path over .rlm files (include/rl_engine.h): rl_mlp on a 9B-shaped dense
+    layer (post norm, gate_up 4096 -> 2 x 12288 with parts gate and up, SwiGLU, down 12288
+    -> 4096 added to h: Engine::encode_mlp, src/engine.mm:943-958) at T = 1 and 5, and on the
+    BASELINE MoE layer (router, routing, experts, combine: encode_moe, :965-1059) at T = 1
+    and 512, in affine files with bf16 scales written here, one model of enough layers that
+    the steps, which rotate over the layers, stream from HBM. Beside each, the sum of its
+    parts timed alone the same way: rl_norm, rl_linear on gate_up, the SwiGLU kernel and
+    rl_linear on down (ACCUM); or rl_norm, rl_linear on the router and the expert kernels
+    (rlq_moe over stacks of the same shapes and scale type packed by the kernel ABI)."""
+    import torch
+
+    from raceline_amd import ops, synth
+    from raceline_amd.configs import MOE, linear_bytes
+    from raceline_amd.model import Engine
+
+    out = {}
+    H, I = 4096, 12288
+    per_layer = linear_bytes(1, H, 2 * I) + linear_bytes(1, I, H)
+    layers = -(-CACHE_DEFEAT_BYTES // per_layer)
+    path = os.path.join(tmpdir, "dense_9b_mlp.rlm")
+    t0 = time.time()
+    synth.write_mlp_model(path, layers, H, I, seed=1)
+    log(f"[bench] wrote a {layers}-layer 9B-shaped MLP model ({os.path.getsize(path) / 1e9:.2f} GB) "
+        f"in {time.time() - t0:.1f} s")
+    with Engine(path, max_chunk=512) as e:
+        for T in (1, 5):
+            h = synth.random_activations(T, H, 40 + T, device).float()
+            xn = torch.empty((T, H), dtype=torch.float16, device=device)
+            g = torch.empty((T, 2 * I), dtype=torch.float32, device=device)
+            act = torch.empty((T, I), dtype=torch.float16, device=device)
+
+            def swiglu():
+                ops.lib.call("rlq_moe_swiglu", g.data_ptr(), g.stride(0), T, I, 0, act.data_ptr(), act.stride(0),
+                             ops._stream())
+
+            parts = {
+                "rl_mlp": [(lambda i=i: e.mlp(i, h)) for i in range(layers)],
+                "norm": [(lambda i=i: lib_norm(e, 1, i, h, xn)) for i in range(layers)],
+                "gate_up": [(lambda i=i: e.linear(f"layers.{i}.mlp.gate_up", xn, out=g)) for i in range(layers)],
+                "swiglu": [swiglu] * layers,
+                "down": [(lambda i=i: e.linear(f"layers.{i}.mlp.down", act, out=h, accum=True)) for i in range(layers)],
+            }
+            times = {k: time_steps(StepGraphs(v), steps, warmup) for k, v in parts.items()}
+            nb = linear_bytes(T, H, 2 * I) + linear_bytes(T, I, H)
+            ent = {k + "_us": round(v * 1e6, 2) for k, v in times.items()}
+            ent["sum_of_parts_us"] = round(sum(v for k, v in times.items() if k != "rl_mlp") * 1e6, 2)
+            ent["GB/s"] = round(nb / times["rl_mlp"] / 1e9, 1)
+            out[f"engine_dense_9b_mlp_t{T}"] = ent
+            log(f"[bench] engine rl_mlp 9B dense T={T}: {ent['rl_mlp_us']} us (parts {ent['sum_of_parts_us']} us)")
+    os.remove(path)
+
+    E, Hm, Im, topk = MOE["E"], MOE["H"], MOE["I"], MOE["topk"]
+    per_layer = ops.packed_bytes(Hm, (E + 1) * 2 * Im) + ops.packed_bytes(Im, (E + 1) * Hm)
+    layers = max(2, -(-CACHE_DEFEAT_BYTES // per_layer))
+    path = os.path.join(tmpdir, "moe_35b.rlm")
+    t0 = time.time()
+    synth.write_mlp_model(path, layers, Hm, experts=E, topk=topk, moe_inter=Im, seed=2)
+    log(f"[bench] wrote a {layers}-layer MoE model ({os.path.getsize(path) / 1e9:.2f} GB) in {time.time() - t0:.1f} s")
+    mws = []
+    for c in range(layers):
+        gu = synth.random_affine((E + 1) * 2 * Im, Hm, 520 + 2 * c, device, packed=False, scale_dtype=torch.bfloat16)
+        dn = synth.random_affine((E + 1) * Hm, Im, 521 + 2 * c, device, packed=False, scale_dtype=torch.bfloat16)
+        mws.append(ops.pack_moe(gu, dn, E, Hm, Im))
+        del gu, dn
+    with Engine(path, max_chunk=512) as e:
+        for T in MOE["tokens"]:
+            # one-token steps draw their own residual rows, so the routing (and the experts
+            # read) changes from step to step, as moe_step_logits explains
+            n = max(MOE_T1_STEPS, layers) if T == 1 else layers
+            hs = [synth.random_activations(T, Hm, 50 + j, device).float() for j in range(n if T == 1 else 1)]
+            hs = hs * n if T > 1 else hs
+            xn = torch.empty((T, Hm), dtype=torch.float16, device=device)
+            lg = torch.empty((T, (E + 1 + 255) // 256 * 256), dtype=torch.float32, device=device)
+            logits = moe_step_logits(T, E, layers, device)
+            ws = torch.empty(ops.moe_workspace_bytes(T, E, topk, Hm, Im), dtype=torch.uint8, device=device)
+            parts = {
+                "rl_mlp": [(lambda j=j: e.mlp(j % layers, hs[j])) for j in range(n)],
+                "norm": [(lambda j=j: lib_norm(e, 1, j % layers, hs[j], xn)) for j in range(n)],
+                "router": [(lambda j=j: e.linear(f"layers.{j % layers}.moe.router", xn, out=lg)) for j in range(n)],
+                "experts": [(lambda j=j: ops.moe(xn, logits[j % len(logits)], mws[j % layers], topk, hs[j],
+                                                 workspace=ws)) for j in range(n)],
+            }
+            times = {k: time_steps(StepGraphs(v), steps, warmup) for k, v in parts.items()}
+            ent = {k + "_us": round(v * 1e6, 2) for k, v in times.items()}
+            ent["sum_of_parts_us"] = round(sum(v for k, v in times.items() if k != "rl_mlp") * 1e6, 2)
+            out[f"engine_moe_t{T}"] = ent
+            log(f"[bench] engine rl_mlp MoE T={T}: {ent['rl_mlp_us']} us (parts {ent['sum_of_parts_us']} us)")
+    del mws
+    os.remove(path)
+    torch.cuda.empty_cache()
+    return out
+
+
+def lib_norm(e, which, layer, h, xn):
+    """rl_norm into a caller's buffer (the engine's Python wrapper allocates its output)."""
+    from raceline_amd import lib
+    from raceline_amd.model import _check, _stream
+
+    _check(lib.load().rl_norm(e._e, which, layer, h.data_ptr(), h.stride(0), h.shape[0], xn.data_ptr(), xn.stride(0),
+                              _stream()), "rl_norm")
 
 
 def bench_prefill(device, steps, warmup):
@@ -442,8 +615,13 @@ def bench_part(part, steps, warmup):
     lib.load()
     dev = torch.device("cuda:0")
     log(f"[bench] part {part}")
+    if part == "engine":
+        import tempfile
+
+        with tempfile.TemporaryDirectory() as tmp:
+            return bench_engine(dev, steps, warmup, tmp)
     fn = {"prefill": bench_prefill, "moe": bench_moe, "decode": bench_decode, "epilogue": bench_native_epilogue,
-          "launch": bench_launch_cost}[part]
+          "launch": bench_launch_cost, "bf16": bench_bf16, "head": bench_head}[part]
     return fn(dev, steps, warmup)
 
 
@@ -746,7 +924,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail configs, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--part", choices=["prefill", "moe", "decode", "epilogue", "launch", "cpu"],
+    ap.add_argument("--part", choices=["prefill", "moe", "decode", "epilogue", "launch", "bf16", "head", "engine",
+                                       "cpu"],
                     help="run only this part of the detail (for rocprofv3); prints its figures as JSON")
     ap.add_argument("--profile", nargs="?", const="gemv", choices=["gemv", "moe", "gemm"],
                     help="launch only the dominant kernel (gemv), the MoE layer at T=512 (moe) or the prefill "
@@ -847,6 +1026,12 @@ def main():
         detail.update(bench_prefill(dev, args.steps, args.warmup))
         detail.update(bench_moe(dev, args.steps, args.warmup))
         detail.update(bench_native_epilogue(dev, args.steps, args.warmup))
+        detail.update(bench_bf16(dev, args.steps, args.warmup))
+        detail.update(bench_head(dev, args.steps, args.warmup))
+        import tempfile
+
+        with tempfile.TemporaryDirectory() as tmp:
+            detail.update(bench_engine(dev, args.steps, args.warmup, tmp))
 
     cpu = None
     if not args.quick and not args.no_cpu:

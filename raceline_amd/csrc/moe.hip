@@ -547,6 +547,54 @@ __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, 
   expert_tile<GPW, SD, 0, true>(a, order[i], i, 1, lds);
 }
 
+// tile_dot_lds for two blocks of 16 staged rows at once (xs: row 0 of the first block, the
+// second 16 rows further; gs: the first block's sums of group wg0, 16 NB = 32 floats per
+// group, the second block's 16 after them). The codes of each group are converted once and
+// multiplied into both blocks; each block's products, sums and order are tile_dot_lds's, so
+// each gets the bits it gets alone. two = false: the second block is empty and skipped.
+template <int GPW, int SD, int SUB, int BOOK = kAffine>
+__device__ __forceinline__ void tile_dot_lds2(const u32x4 (&wq)[GPW / 2], const u32x4 (&sq)[GPW / 4],
+                                              const _Float16 *xs, const float *gs, int rstride, int wn, int lane,
+                                              bool two, f32x4 (&acc0)[SUB], f32x4 (&acc1)[SUB]) {
+  const _Float16 *xa0 = xs + (lane & 15) * rstride + 8 * (lane >> 4);
+  const _Float16 *xa1 = xa0 + 16 * rstride;
+  const float *ga0 = gs + 4 * (lane >> 4);
+  const float *ga1 = ga0 + 16;
+#pragma unroll
+  for (int s = 0; s < SUB; ++s) {
+    acc0[s] = f32x4{};
+    acc1[s] = f32x4{};
+  }
+#pragma unroll
+  for (int jg = 0; jg < GPW; ++jg) {
+    if (jg < wn) {   // uniform: the groups past the wave's range add nothing
+      constexpr int per = GPW / SUB;
+      half8 bq[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t u = wq[jg >> 1][2 * (jg & 1) + s];
+        if constexpr (BOOK == kAffine) bq[s] = nib8_to_half8_sub(u);
+        else bq[s] = native8_operand<BOOK>(u);
+      }
+      auto block = [&](const _Float16 *xa, const float *ga, f32x4 &acc) {
+        half8 af[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(xa + jg * kGroup + 32 * s);
+        if constexpr (BOOK == kAffine) {
+          const f32x4 gsv = *reinterpret_cast<const f32x4 *>(ga + 32 * jg);
+          group_step_gs_b<GPW, SD, 4>(acc, af, gsv, bq, sq, jg);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 2; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bq[s], acc, 0, 0, 0);
+        }
+        asm volatile("" : "+v"(acc));
+      };
+      block(xa0, ga0, acc0[jg / per]);
+      if (two) block(xa1, ga1, acc1[jg / per]);   // uniform
+    }
+  }
+}
+
 // The same products with the item's token rows staged once per workgroup: a workgroup
 // takes one work item and `tiles_per_block` consecutive 16-row weight tiles of its expert,
 // each split over K between `waves_per_tile` waves (wave = tile * waves_per_tile + part).
@@ -567,10 +615,21 @@ __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, 
 // BOOK: kAffine, or (KIND 1 only) a native book: expert e's matrix sits at slot
 // a.slots[e] with row scales a.s_row, the products chain as moe_native_kernel's do and the
 // row scale is applied at the store (a slot outside the table gives zero rows).
-template <int GPW, int SD, int KIND, int CPL, int SUB, int BOOK = kAffine>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 6 : 1))) void moe_expert_lds_kernel(
-    MoeArgs a) {
+// NB = 2: an expert's first two work items run in one workgroup as two blocks of 16 rows
+// (item i leads when the item before it belongs to another expert, and takes item i + 1 when
+// that one is its expert's too; the second item's own workgroup leaves at once). Both blocks
+// use the codes as converted once, and each block's products, sums and order are those of
+// the item alone, so the bits do not change; what it saves is the second reading and
+// conversion of the expert's weights, which otherwise a few rows pay in full (at T = 512,
+// 120 of the 256 routed experts have a second item, of 3.3 rows on average). An expert's
+// third and later items (only the shared expert has them at these sizes) run alone.
+// LDS with NB blocks: 16 NB rows, the group sums [G][16 NB], the partials of NB blocks.
+template <int GPW, int SD, int KIND, int CPL, int SUB, int BOOK = kAffine, int NB = 1>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 && NB == 1 ? 6 : 1))) void
+moe_expert_lds_kernel(MoeArgs a) {
   static_assert(BOOK == kAffine || KIND == 1, "native books: the down kind only");
+  static_assert(NB == 1 || NB == 2, "one or two row blocks");
+  constexpr int NR = 16 * NB;                     // staged rows
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int item = blockIdx.y;
   // the item entry is read together with the count (the list holds the most items a call
@@ -582,6 +641,20 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
   const int4 ic = clamp_item(it, a.n_experts, a.n_rows);
   int e = ic.x;
   const int r0 = ic.y, rows = ic.z;
+  int r1 = 0, rows1 = 0;                        // the second block (NB = 2): its first row and count
+  if constexpr (NB == 2) {
+    const int ep = item > 0 ? a.items[item - 1].x : -1;
+    const int ep2 = item > 1 ? a.items[item - 2].x : -1;
+    if (ep == it.x && ep2 != it.x) return;      // uniform: the second item of its expert, taken by the first
+    if (ep != it.x && item + 1 < n_items) {
+      const int4 nx = a.items[item + 1];
+      if (nx.x == it.x) {
+        const int4 nc = clamp_item(nx, a.n_experts, a.n_rows);
+        r1 = nc.y;
+        rows1 = nc.z;
+      }
+    }
+  }
   bool slot_ok = true;
   if constexpr (BOOK != kAffine) {
     const int slot = __builtin_amdgcn_readfirstlane(a.slots[e]);
@@ -602,16 +675,23 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
   const int wn = tile_ok ? max(0, min(G, wg0 + GPW) - wg0) : 0;
   const int rstride = a.K + 8;
   _Float16 *xs = reinterpret_cast<_Float16 *>(lds);
-  float *gsl = reinterpret_cast<float *>(lds + (size_t)16 * rstride * 2);
-  f32x4 *red = reinterpret_cast<f32x4 *>(gsl + (size_t)G * 16);
+  float *gsl = reinterpret_cast<float *>(lds + (size_t)NR * rstride * 2);
+  f32x4 *red = reinterpret_cast<f32x4 *>(gsl + (size_t)G * NR);
   const int nw = nthreads >> 6, cpr = a.K / 8;
 
   // 1. the wave's first row (lane l: chunks l, l + 64, ... of 8 halves); rows past the
-  // item's read zeros
+  // item's read zeros. Staged row r < 16 is row r of the first block, r >= 16 row r - 16 of
+  // the second.
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)((size_t)a.x_rows * a.x_stride * 2));
   auto load_row = [&](int row, u32x4 (&xr)[CPL]) {
-    const bool ok = row < rows;
-    const int src = KIND == 0 ? token_of(a.tok, r0 + (ok ? row : 0), a.x_rows) : r0 + row;
+    int blk_r0 = r0, blk_rows = rows, br = row;
+    if constexpr (NB == 2) {
+      blk_r0 = row < 16 ? r0 : r1;
+      blk_rows = row < 16 ? rows : rows1;
+      br = row & 15;
+    }
+    const bool ok = br < blk_rows;
+    const int src = KIND == 0 ? token_of(a.tok, blk_r0 + (ok ? br : 0), a.x_rows) : blk_r0 + br;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = lane + 64 * j;
@@ -634,69 +714,84 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 ? 
   issue_tile_loads<GPW, BOOK>(wt, lane, wq, sq);
   __builtin_amdgcn_sched_barrier(0);
   // 3. rows -> LDS in operand order (loads complete in issue order: the first row waits
-  // for its own loads only); a workgroup of fewer than 16 waves stages the rest in turn
+  // for its own loads only); a workgroup of fewer than NR waves stages the rest in turn
   store_row(wave, xr);
-  for (int row = wave + nw; row < 16; row += nw) {
+  for (int row = wave + nw; row < NR; row += nw) {
     load_row(row, xr);
     store_row(row, xr);
   }
   __syncthreads();
-  // 4. the group sums of the 16 rows, once for every tile: wave w forms groups w, w + nw, ...
-  for (int g = wave; BOOK == kAffine && g < G; g += nw) {
-    const _Float16 *xa = xs + (size_t)c16 * rstride + 8 * j4 + (size_t)g * kGroup;
+  // 4. the group sums of the staged rows, once for every tile: wave w forms groups w, w + nw,
+  // ... of each block
+  for (int gb = wave; BOOK == kAffine && gb < G * NB; gb += nw) {
+    const int b = NB == 1 ? 0 : gb >= G, g = gb - b * G;
+    const _Float16 *xa = xs + (size_t)(16 * b + c16) * rstride + 8 * j4 + (size_t)g * kGroup;
     half8 af[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) af[s] = *reinterpret_cast<const half8 *>(xa + 32 * s);
     const f32x4 gsv = group_sums(af);
-    if (c16 == 0) *reinterpret_cast<f32x4 *>(gsl + (size_t)g * 16 + 4 * j4) = gsv;
+    if (c16 == 0) *reinterpret_cast<f32x4 *>(gsl + (size_t)g * NR + 16 * b + 4 * j4) = gsv;
   }
   __syncthreads();
   // 5. products, then the sub-parts of each tile meet in order (only those with groups)
-  f32x4 accs[SUB];
-  tile_dot_lds<GPW, SD, SUB, BOOK>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn, lane, accs);
+  f32x4 accs[NB][SUB];
+  if constexpr (NB == 1) {
+    tile_dot_lds<GPW, SD, SUB, BOOK>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn, lane,
+                                     accs[0]);
+  } else {
+    tile_dot_lds2<GPW, SD, SUB, BOOK>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * NR, rstride, wn, lane,
+                                      rows1 > 0, accs[0], accs[1]);
+  }
   constexpr int per = GPW / SUB;
   if (part > 0) {
 #pragma unroll
-    for (int s = 0; s < SUB; ++s) red[(((size_t)tt * (W - 1) + part - 1) * SUB + s) * 64 + lane] = accs[s];
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int s = 0; s < SUB; ++s) red[((((size_t)tt * (W - 1) + part - 1) * NB + b) * SUB + s) * 64 + lane] = accs[b][s];
   }
   __syncthreads();
   if (part != 0 || !tile_ok) return;
-  f32x4 acc = accs[0];
 #pragma unroll
-  for (int s = 1; s < SUB; ++s) {
-    if (s * per < G) {
+  for (int b = 0; b < NB; ++b) {
+    const int br0 = b ? r1 : r0, brows = b ? rows1 : rows;
+    if (b > 0 && brows == 0) continue;            // uniform: no second block
+    f32x4 acc = accs[b][0];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[v] += accs[s][v];
+    for (int s = 1; s < SUB; ++s) {
+      if (s * per < G) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] += accs[b][s][v];
+      }
     }
-  }
-  for (int p = 1; p < W; ++p) {
+    for (int p = 1; p < W; ++p) {
 #pragma unroll
-    for (int s = 0; s < SUB; ++s) {
-      if ((p * SUB + s) * per >= G) break;
-      const f32x4 o = red[(((size_t)tt * (W - 1) + p - 1) * SUB + s) * 64 + lane];
+      for (int s = 0; s < SUB; ++s) {
+        if ((p * SUB + s) * per >= G) break;
+        const f32x4 o = red[((((size_t)tt * (W - 1) + p - 1) * NB + b) * SUB + s) * 64 + lane];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[v] += o[v];
+        for (int v = 0; v < 4; ++v) acc[v] += o[v];
+      }
     }
-  }
-  if constexpr (KIND == 0) {
-    _Float16 *act = static_cast<_Float16 *>(a.out);
+    if constexpr (KIND == 0) {
+      _Float16 *act = static_cast<_Float16 *>(a.out);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float u = __shfl_xor(acc[v], 8);
-      const int r = 4 * j4 + v;
-      if (c16 < 8 && r < rows)
-        act[(size_t)(r0 + r) * a.out_stride + 8 * tile + c16] = static_cast<_Float16>(silu(acc[v]) * u);
-    }
-  } else {
-    float *y = static_cast<float *>(a.out);
-    float sn = 1.0f;
-    if constexpr (BOOK != kAffine) sn = a.s_row[(size_t)e * a.tiles_per_expert * 16 + 16 * tile + c16];
+      for (int v = 0; v < 4; ++v) {
+        const float u = __shfl_xor(acc[v], 8);
+        const int r = 4 * j4 + v;
+        if (c16 < 8 && r < brows)
+          act[(size_t)(br0 + r) * a.out_stride + 8 * tile + c16] = static_cast<_Float16>(silu(acc[v]) * u);
+      }
+    } else {
+      float *y = static_cast<float *>(a.out);
+      float sn = 1.0f;
+      if constexpr (BOOK != kAffine) sn = a.s_row[(size_t)e * a.tiles_per_expert * 16 + 16 * tile + c16];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int r = 4 * j4 + v;
-      if (r < rows)
-        y[(size_t)(r0 + r) * a.out_stride + 16 * tile + c16] =
-            BOOK == kAffine ? acc[v] : slot_ok ? sn * acc[v] : 0.0f;
+      for (int v = 0; v < 4; ++v) {
+        const int r = 4 * j4 + v;
+        if (r < brows)
+          y[(size_t)(br0 + r) * a.out_stride + 16 * tile + c16] =
+              BOOK == kAffine ? acc[v] : slot_ok ? sn * acc[v] : 0.0f;
+      }
     }
   }
 }
@@ -837,37 +932,62 @@ static int staged_gpw(int K) { return K <= 1024 ? 8 : 16; }
 // groups per wave (about 52 VGPRs) two workgroups of 16 waves fit. Measured on the MoE
 // layer at T = 512 (H = 2048, I = 512): gate/up 206 -> 184 us per layer going from 16 to
 // 12 waves; 8 and 16 waves for down within 2 us.
-static int staged_waves(int gpw, int W, int sub, size_t lds_rows) {
-  const size_t lds12 = lds_rows + (size_t)(12 / W) * (W - 1) * sub * 64 * 16;   // a 12-wave workgroup
+static int staged_waves(int gpw, int W, int sub, int nb, size_t lds_rows) {
+  const size_t lds12 = lds_rows + (size_t)(12 / W) * (W - 1) * nb * sub * 64 * 16;   // a 12-wave workgroup
   return gpw == 16 && 2 * lds12 <= kMaxLdsBytes ? 12 : 16;
 }
 
-template <int GPW, int SD, int KIND, int SUB, int BOOK = kAffine>
-static int launch_staged_inst(int tpe, hipStream_t st, MoeArgs a, int items) {
+// LDS of the staged kernel: NB blocks of 16 rows of K + 8 halves, their group sums, and the
+// partials of parts 1.. of tpb tiles
+static size_t staged_lds_bytes(int K, int GPW, int SUB, int NB, int tpb) {
+  const int G = K / kGroup, W = (G + GPW - 1) / GPW;
+  return (size_t)16 * NB * (K + 8) * 2 + (size_t)G * 16 * NB * 4 + (size_t)tpb * (W - 1) * NB * SUB * 64 * 16;
+}
+
+// tiles per workgroup: as many as staged_waves allows, fewer where the LDS would not hold them
+static int staged_tpb(int K, int GPW, int SUB, int NB, int tpe) {
+  const int G = K / kGroup, W = (G + GPW - 1) / GPW;
+  int tpb = std::max(1, std::min(tpe, staged_waves(GPW, W, SUB, NB, staged_lds_bytes(K, GPW, SUB, NB, 0)) / W));
+  while (tpb > 1 && staged_lds_bytes(K, GPW, SUB, NB, tpb) > kMaxLdsBytes) --tpb;
+  return tpb;
+}
+
+template <int GPW, int SD, int KIND, int SUB, int BOOK, int NB>
+static int launch_staged_nb(int tpe, hipStream_t st, MoeArgs a, int items) {
   const int G = a.K / kGroup, W = (G + GPW - 1) / GPW;
-  const size_t lds_rows = (size_t)16 * (a.K + 8) * 2 + (size_t)G * 16 * 4;
-  const int tpb = std::max(1, std::min(tpe, staged_waves(GPW, W, SUB, lds_rows) / W));
+  const int tpb = staged_tpb(a.K, GPW, SUB, NB, tpe);
   a.tiles_per_block = tpb;
   a.waves_per_tile = W;
   const int threads = 64 * W * tpb;
   const int xpt = (a.K / 8 + 63) / 64;   // chunks of 8 halves per lane and row
-  const size_t lds = lds_rows + (size_t)tpb * (W - 1) * SUB * 64 * 16;
+  const size_t lds = staged_lds_bytes(a.K, GPW, SUB, NB, tpb);
+  RLQ_REQUIRE(lds <= kMaxLdsBytes, "moe: the staged kernel needs %zu bytes of LDS (K=%d)", lds, a.K);
   const dim3 grid((tpe + tpb - 1) / tpb, items);
   static LdsOptIn lds_opt[4];
-  const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK>)};
+  const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK, NB>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK, NB>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK, NB>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK, NB>)};
   const int which = xpt <= 1 ? 0 : xpt <= 2 ? 1 : xpt <= 4 ? 2 : 3;
   if (xpt <= 8)
     if (int rc = allow_large_lds(fns[which], lds_opt[which])) return rc;
-  if (xpt <= 1) moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 2) moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 4) moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 8) moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK><<<grid, threads, lds, st>>>(a);
+  if (xpt <= 1) moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK, NB><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 2) moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK, NB><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 4) moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK, NB><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 8) moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK, NB><<<grid, threads, lds, st>>>(a);
   else return fail("moe: %d activation chunks per thread (K=%d) is more than the staged kernel takes", xpt, a.K);
   RLQ_HIP(hipGetLastError());
   return 0;
+}
+
+template <int GPW, int SD, int KIND, int SUB, int BOOK = kAffine>
+static int launch_staged_inst(int tpe, hipStream_t st, MoeArgs a, int items) {
+  // Two row blocks per workgroup for the down projection, where the LDS holds them (measured
+  // at T = 512: 180.1 and 181.2 -> 179.8 and 178.0 us per layer, alternating on one box). Not
+  // for gate/up: 32 rows of K = 2048 leave room for one workgroup per CU (224 us per layer).
+  const bool pair = KIND == 1 && staged_lds_bytes(a.K, GPW, SUB, 2, staged_tpb(a.K, GPW, SUB, 2, tpe)) <= kMaxLdsBytes;
+  if (pair) return launch_staged_nb<GPW, SD, KIND, SUB, BOOK, 2>(tpe, st, a, items);
+  return launch_staged_nb<GPW, SD, KIND, SUB, BOOK, 1>(tpe, st, a, items);
 }
 
 template <int KIND>

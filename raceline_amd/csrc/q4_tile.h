@@ -202,6 +202,21 @@ __device__ __forceinline__ void group_step_gs(f32x4 &acc, const half8 (&af)[2], 
   for (int r = 0; r < NACC; ++r) acc[r] = fma_scale<SD, 1>(pr, gsv[r], __builtin_fmaf(sc, p[r], acc[r]));
 }
 
+// group_step_gs with the group's two B operands already converted (bq[s] =
+// nib8_to_half8_sub of word 2 (jg & 1) + s of wq[jg >> 1]): the same operations, for a
+// caller that multiplies the same codes into several blocks of rows.
+template <int GPW, int SD, int NACC>
+__device__ __forceinline__ void group_step_gs_b(f32x4 &acc, const half8 (&af)[2], const f32x4 &gsv,
+                                                const half8 (&bq)[2], const u32x4 (&sq)[GPW / 4], int jg) {
+  f32x4 p = {};
+#pragma unroll
+  for (int s = 0; s < 2; ++s) p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bq[s], p, 0, 0, 0);
+  const uint32_t pr = sq[jg >> 2][jg & 3];
+  const float sc = fma_scale<SD, 0>(pr, kTwo24, 0.0f);   // s * 2^24, exact: undoes the codes' 2^-24
+#pragma unroll
+  for (int r = 0; r < NACC; ++r) acc[r] = fma_scale<SD, 1>(pr, gsv[r], __builtin_fmaf(sc, p[r], acc[r]));
+}
+
 // One group jg of the wave's part: acc[r] += s * (x . q) + b * gsum for the first NACC
 // accumulator rows (NACC = 1 when only token row 0 is live).
 template <int GPW, int SD, int NACC>

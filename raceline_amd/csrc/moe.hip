@@ -552,7 +552,7 @@ __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, 
 // group, the second block's 16 after them). The codes of each group are converted once and
 // multiplied into both blocks; each block's products, sums and order are tile_dot_lds's, so
 // each gets the bits it gets alone. two = false: the second block is empty and skipped.
-template <int GPW, int SD, int SUB, int BOOK = kAffine>
+template <int GPW, int SD, int SUB, int BOOK = kAffine, bool FULL = false>
 __device__ __forceinline__ void tile_dot_lds2(const u32x4 (&wq)[GPW / 2], const u32x4 (&sq)[GPW / 4],
                                               const _Float16 *xs, const float *gs, int rstride, int wn, int lane,
                                               bool two, f32x4 (&acc0)[SUB], f32x4 (&acc1)[SUB]) {
@@ -567,7 +567,7 @@ __device__ __forceinline__ void tile_dot_lds2(const u32x4 (&wq)[GPW / 2], const 
   }
 #pragma unroll
   for (int jg = 0; jg < GPW; ++jg) {
-    if (jg < wn) {   // uniform: the groups past the wave's range add nothing
+    if (FULL || jg < wn) {   // uniform: the groups past the wave's range add nothing (FULL: wn == GPW)
       constexpr int per = GPW / SUB;
       half8 bq[2];
 #pragma unroll
@@ -624,7 +624,7 @@ __device__ __forceinline__ void tile_dot_lds2(const u32x4 (&wq)[GPW / 2], const 
 // 120 of the 256 routed experts have a second item, of 3.3 rows on average). An expert's
 // third and later items (only the shared expert has them at these sizes) run alone.
 // LDS with NB blocks: 16 NB rows, the group sums [G][16 NB], the partials of NB blocks.
-template <int GPW, int SD, int KIND, int CPL, int SUB, int BOOK = kAffine, int NB = 1>
+template <int GPW, int SD, int KIND, int CPL, int SUB, int BOOK = kAffine, int NB = 1, bool FULL = false>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(CPL < 8 && NB == 1 ? 6 : 1))) void
 moe_expert_lds_kernel(MoeArgs a) {
   static_assert(BOOK == kAffine || KIND == 1, "native books: the down kind only");
@@ -736,8 +736,28 @@ moe_expert_lds_kernel(MoeArgs a) {
   // 5. products, then the sub-parts of each tile meet in order (only those with groups)
   f32x4 accs[NB][SUB];
   if constexpr (NB == 1) {
-    tile_dot_lds<GPW, SD, SUB, BOOK>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn, lane,
-                                     accs[0]);
+    if constexpr (FULL) {
+      // every part of K holds GPW groups: the only wave without groups is one past the
+      // expert's last tile
+      if (wn > 0) {   // uniform
+        tile_dot_lds<GPW, SD, SUB, BOOK, true>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn,
+                                               lane, accs[0]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < SUB; ++s) accs[0][s] = f32x4{};
+      }
+    } else {
+      tile_dot_lds<GPW, SD, SUB, BOOK>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * 16, rstride, wn, lane,
+                                       accs[0]);
+    }
+  } else if constexpr (FULL) {
+    if (wn > 0) {   // uniform
+      tile_dot_lds2<GPW, SD, SUB, BOOK, true>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * NR, rstride, wn,
+                                              lane, rows1 > 0, accs[0], accs[1]);
+    } else {
+#pragma unroll
+      for (int s = 0; s < SUB; ++s) accs[0][s] = accs[1][s] = f32x4{};
+    }
   } else {
     tile_dot_lds2<GPW, SD, SUB, BOOK>(wq, sq, xs + (size_t)wg0 * kGroup, gsl + (size_t)wg0 * NR, rstride, wn, lane,
                                       rows1 > 0, accs[0], accs[1]);
@@ -952,7 +972,7 @@ static int staged_tpb(int K, int GPW, int SUB, int NB, int tpe) {
   return tpb;
 }
 
-template <int GPW, int SD, int KIND, int SUB, int BOOK, int NB>
+template <int GPW, int SD, int KIND, int SUB, int BOOK, int NB, bool FULL = false>
 static int launch_staged_nb(int tpe, hipStream_t st, MoeArgs a, int items) {
   const int G = a.K / kGroup, W = (G + GPW - 1) / GPW;
   const int tpb = staged_tpb(a.K, GPW, SUB, NB, tpe);
@@ -964,17 +984,17 @@ static int launch_staged_nb(int tpe, hipStream_t st, MoeArgs a, int items) {
   RLQ_REQUIRE(lds <= kMaxLdsBytes, "moe: the staged kernel needs %zu bytes of LDS (K=%d)", lds, a.K);
   const dim3 grid((tpe + tpb - 1) / tpb, items);
   static LdsOptIn lds_opt[4];
-  const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK, NB>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK, NB>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK, NB>),
-                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK, NB>)};
+  const void *fns[4] = {reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK, NB, FULL>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK, NB, FULL>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK, NB, FULL>),
+                        reinterpret_cast<const void *>(&moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK, NB, FULL>)};
   const int which = xpt <= 1 ? 0 : xpt <= 2 ? 1 : xpt <= 4 ? 2 : 3;
   if (xpt <= 8)
     if (int rc = allow_large_lds(fns[which], lds_opt[which])) return rc;
-  if (xpt <= 1) moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK, NB><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 2) moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK, NB><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 4) moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK, NB><<<grid, threads, lds, st>>>(a);
-  else if (xpt <= 8) moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK, NB><<<grid, threads, lds, st>>>(a);
+  if (xpt <= 1) moe_expert_lds_kernel<GPW, SD, KIND, 1, SUB, BOOK, NB, FULL><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 2) moe_expert_lds_kernel<GPW, SD, KIND, 2, SUB, BOOK, NB, FULL><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 4) moe_expert_lds_kernel<GPW, SD, KIND, 4, SUB, BOOK, NB, FULL><<<grid, threads, lds, st>>>(a);
+  else if (xpt <= 8) moe_expert_lds_kernel<GPW, SD, KIND, 8, SUB, BOOK, NB, FULL><<<grid, threads, lds, st>>>(a);
   else return fail("moe: %d activation chunks per thread (K=%d) is more than the staged kernel takes", xpt, a.K);
   RLQ_HIP(hipGetLastError());
   return 0;
@@ -986,8 +1006,14 @@ static int launch_staged_inst(int tpe, hipStream_t st, MoeArgs a, int items) {
   // at T = 512: 180.1 and 181.2 -> 179.8 and 178.0 us per layer, alternating on one box). Not
   // for gate/up: 32 rows of K = 2048 leave room for one workgroup per CU (224 us per layer).
   const bool pair = KIND == 1 && staged_lds_bytes(a.K, GPW, SUB, 2, staged_tpb(a.K, GPW, SUB, 2, tpe)) <= kMaxLdsBytes;
-  if (pair) return launch_staged_nb<GPW, SD, KIND, SUB, BOOK, 2>(tpe, st, a, items);
-  return launch_staged_nb<GPW, SD, KIND, SUB, BOOK, 1>(tpe, st, a, items);
+  // every part of K whole (G a multiple of GPW, as at every BASELINE shape): the kernel
+  // without per-group branches (the same bits; the gate/up kernel's VALU instructions 848 ->
+  // 661, the register moves of the branches' merge points 211 -> 29)
+  const bool full = (a.K / kGroup) % GPW == 0;
+  if (pair) return full ? launch_staged_nb<GPW, SD, KIND, SUB, BOOK, 2, true>(tpe, st, a, items)
+                        : launch_staged_nb<GPW, SD, KIND, SUB, BOOK, 2>(tpe, st, a, items);
+  return full ? launch_staged_nb<GPW, SD, KIND, SUB, BOOK, 1, true>(tpe, st, a, items)
+              : launch_staged_nb<GPW, SD, KIND, SUB, BOOK, 1>(tpe, st, a, items);
 }
 
 template <int KIND>

@@ -511,7 +511,10 @@ __device__ __forceinline__ f32x4 tile_dot_rows_staged(const WaveTile &w, __amdgp
 // GPW / SUB groups per wave sums the same groups.
 // BOOK: kAffine, or a native book (int15, fp4), whose products chain in the MFMA over each
 // sub-part (no per-group scale or group sums; gs unused), as tile_dot_rows chains them.
-template <int GPW, int SD, int SUB, int BOOK = kAffine>
+// FULL: the caller guarantees wn == GPW (every group of the range is real), and the loop runs
+// with no per-group branch: straight-line code, without the register moves that the
+// branches' merge points cost (about 4 per group), with the same products in the same order.
+template <int GPW, int SD, int SUB, int BOOK = kAffine, bool FULL = false>
 __device__ __forceinline__ void tile_dot_lds(const u32x4 (&wq)[GPW / 2], const u32x4 (&sq)[GPW / 4],
                                              const _Float16 *xs, const float *gs, int rstride, int wn, int lane,
                                              f32x4 (&acc)[SUB]) {
@@ -521,7 +524,7 @@ __device__ __forceinline__ void tile_dot_lds(const u32x4 (&wq)[GPW / 2], const u
   for (int s = 0; s < SUB; ++s) acc[s] = f32x4{};
 #pragma unroll
   for (int jg = 0; jg < GPW; ++jg) {
-    if (jg < wn) {   // uniform: the groups past the wave's range add nothing
+    if (FULL || jg < wn) {   // uniform: the groups past the wave's range add nothing
       constexpr int per = GPW / SUB;
       half8 af[2];
 #pragma unroll

@@ -75,17 +75,11 @@ static int dev_alloc(DevMem &m, size_t bytes, const char *what) {
 
 constexpr int kNormThreads = 256;
 
-// out[r][i] = half(h[r][i] * inv * w[i]), inv = 1 / sqrt(sum_i h[r][i]^2 / D + eps): one
-// workgroup per row. Each thread sums its elements i = tid, tid + 256, ... in order; the
-// threads' sums meet in a fixed tree (butterfly in each wave, then the waves in order), so
-// a row's result depends on nothing but the row (the property kernels/ops.metal:60-72 keeps
-// for chunking).
-__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *h, int h_stride, const float *w, int D,
-                                                                float eps, _Float16 *out, int out_stride) {
-  __shared__ float part[kNormThreads / 64];
-  const float *x = h + (size_t)blockIdx.x * h_stride;
-  float ss = 0.0f;
-  for (int i = threadIdx.x; i < D; i += kNormThreads) ss = __builtin_fmaf(x[i], x[i], ss);
+constexpr int kNormMaxPer = 32;   // rows of up to 8192 take the register form
+
+// The sum of the threads' partial sums of squares, in a fixed tree (butterfly in each wave,
+// then the waves in order); every thread gets it.
+__device__ __forceinline__ float norm_total(float ss, float *part) {
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) ss += __shfl_xor(ss, d);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
@@ -93,16 +87,55 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *h, 
   float total = 0.0f;
 #pragma unroll
   for (int wv = 0; wv < kNormThreads / 64; ++wv) total += part[wv];
-  const float inv = 1.0f / __builtin_sqrtf(total / (float)D + eps);
+  return total;
+}
+
+// out[r][i] = half(h[r][i] * inv * w[i]), inv = 1 / sqrt(sum_i h[r][i]^2 / D + eps): one
+// workgroup per row. Each thread sums its elements i = tid, tid + 256, ... in order, and
+// the threads' sums meet in norm_total's tree, so a row's result depends on nothing but the
+// row (the property kernels/ops.metal:60-72 keeps for chunking). With PER > 0 (D <= 256 PER)
+// a thread issues the loads of all its elements of h and w at once and keeps them in
+// registers (buffer loads whose range check returns 0 past D; a zero adds nothing to the
+// sum of squares), so the row costs one memory round trip instead of one per element; the
+// arithmetic is the same. PER = 0 is the loop form for longer rows.
+template <int PER>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *h, int h_stride, const float *w, int D,
+                                                                float eps, _Float16 *out, int out_stride) {
+  __shared__ float part[kNormThreads / 64];
+  const float *x = h + (size_t)blockIdx.x * h_stride;
   _Float16 *o = out + (size_t)blockIdx.x * out_stride;
-  for (int i = threadIdx.x; i < D; i += kNormThreads) o[i] = static_cast<_Float16>(x[i] * inv * w[i]);
+  float ss = 0.0f;
+  if constexpr (PER > 0) {
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)D * 4u), rw = make_rsrc(w, (uint32_t)D * 4u);
+    float xv[PER], wv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      xv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            rx, 4u * (threadIdx.x + (uint32_t)j * kNormThreads), 0, 0));
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      wv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            rw, 4u * (threadIdx.x + (uint32_t)j * kNormThreads), 0, 0));
+#pragma unroll
+    for (int j = 0; j < PER; ++j) ss = __builtin_fmaf(xv[j], xv[j], ss);
+    const float inv = 1.0f / __builtin_sqrtf(norm_total(ss, part) / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = threadIdx.x + j * kNormThreads;
+      if (i < D) o[i] = static_cast<_Float16>(xv[j] * inv * wv[j]);
+    }
+  } else {
+    for (int i = threadIdx.x; i < D; i += kNormThreads) ss = __builtin_fmaf(x[i], x[i], ss);
+    const float inv = 1.0f / __builtin_sqrtf(norm_total(ss, part) / (float)D + eps);
+    for (int i = threadIdx.x; i < D; i += kNormThreads) o[i] = static_cast<_Float16>(x[i] * inv * w[i]);
+  }
 }
 
 // Top-k with rl_top_k's order (value descending, equal values by index ascending, NaN left
-// out), in two passes. Pass 1: workgroup b takes entries [b C, (b+1) C) and picks its k
-// best by k rounds of a workgroup-wide best (each thread holds its entries in registers and
-// marks the ones taken); pass 2: one workgroup picks the k best of all the candidates the
-// same way. A round's best: the larger value, then the lower index.
+// out). Pass 1: workgroup b takes entries [b C, (b+1) C) and picks its k best by k rounds
+// of a workgroup-wide best (each thread holds its entries in registers and marks the ones
+// taken); merge passes then pick the k best of groups of candidates the same way until one
+// workgroup is left. A round's best: the larger value, then the lower index.
 constexpr int kTopkThreads = 256;
 constexpr int kTopkPer = 8;                                  // entries per thread in pass 1
 constexpr int kTopkChunk = kTopkThreads * kTopkPer;          // C
@@ -481,7 +514,15 @@ static int linear_rows(rl_engine *e, const EngineTensor &t, int r0, int N, const
 static int norm_with(rl_engine *e, const float *w, const float *h, int h_stride, int rows, _Float16 *xn,
                      int xn_stride, hipStream_t st) {
   const ModelConfig &c = e->model->config();
-  rms_norm_kernel<<<rows, kNormThreads, 0, st>>>(h, h_stride, w, c.hidden, c.norm_eps, xn, xn_stride);
+  const int per = (c.hidden + kNormThreads - 1) / kNormThreads;
+  auto launch = [&](auto kernel) {
+    kernel<<<rows, kNormThreads, 0, st>>>(h, h_stride, w, c.hidden, c.norm_eps, xn, xn_stride);
+  };
+  if (per <= 8) launch(rms_norm_kernel<8>);
+  else if (per <= 16) launch(rms_norm_kernel<16>);
+  else if (per <= 20) launch(rms_norm_kernel<20>);
+  else if (per <= kNormMaxPer) launch(rms_norm_kernel<kNormMaxPer>);
+  else launch(rms_norm_kernel<0>);
   RLQ_HIP(hipGetLastError());
   return 0;
 }

@@ -444,8 +444,11 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 // waves, each a range of GPW groups of K; the waves meet in LDS in wave order and wave 0
 // writes. KIND 0: gate/up with the gather and SwiGLU fused (interleaved stack); the rows'
 // tokens come from the row -> token map, or (ONE_TOKEN) are all token 0. KIND 1: down.
-template <int GPW, int SD, int KIND, bool ONE_TOKEN>
-__device__ __forceinline__ void expert_tile(const MoeArgs &a, int e, int r0, int rows, unsigned char *lds) {
+// ONE_TOKEN forms accumulator row 0 only; with PRE it takes the token's group sums from gs
+// (all groups of K, formed by row0_group_sums).
+template <int GPW, int SD, int KIND, bool ONE_TOKEN, bool PRE = false>
+__device__ __forceinline__ void expert_tile(const MoeArgs &a, int e, int r0, int rows, unsigned char *lds,
+                                            const float *gs = nullptr) {
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -462,7 +465,8 @@ __device__ __forceinline__ void expert_tile(const MoeArgs &a, int e, int r0, int
   if constexpr (KIND == 0) xrow = ONE_TOKEN ? 0 : token_of(a.tok, xrow, a.x_rows);
   const uint32_t xrange = wn > 0 ? (uint32_t)((a.x_rows - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
-  f32x4 acc = tile_dot_rows<GPW, SD>(wt, rx, (uint32_t)xrow * a.x_stride * 2u + 16u * j4, live, wn, lane);
+  f32x4 acc = tile_dot_rows<GPW, SD, kAffine, ONE_TOKEN ? 1 : 4, PRE>(
+      wt, rx, (uint32_t)xrow * a.x_stride * 2u + 16u * j4, live, wn, lane, PRE ? gs + min(wg0, G) : nullptr);
   acc = reduce_waves(acc, reinterpret_cast<f32x4 *>(lds), wave, waves, lane);
   if (wave != 0) return;
   if constexpr (KIND == 0) {
@@ -506,8 +510,10 @@ __global__ __launch_bounds__(1024) void moe_expert_kernel(MoeArgs a) {
 // number, so item i (= blockIdx.y, S of them) is the i-th smallest chosen expert, at row i;
 // the shared expert, number E, is always the last, so its workgroups skip the routing.
 // Workgroup (0, 0) also writes the routing tables (sel, w, tok, inv, items, n_items) as the
-// sort writes them for one token, for the down and combine launch. LDS: the reduction, then
-// sel [S], w [S] and the chosen experts in ascending order [S].
+// sort writes them for one token, for the down and combine launch. While wave 0 routes, the
+// other waves form the token's group sums for every wave's range (the products then need
+// only the code MFMAs). LDS: the reduction, then sel [S], w [S], the chosen experts in
+// ascending order [S] and the group sums [K / 64].
 template <int GPW, int SD, int EPL>
 __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, const float *logits, int E, int topk,
                                                                      int norm_topk, int *sel, float *w, int *tok,
@@ -524,7 +530,21 @@ __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, 
   int *sel_l = reinterpret_cast<int *>(lds + (size_t)(waves - 1) * 64 * 16);
   float *w_l = reinterpret_cast<float *>(sel_l + S);
   int *order = reinterpret_cast<int *>(w_l + S);   // the chosen experts in ascending order
-  if (threadIdx.x < 64) topk_token<EPL>(logits, E, topk, norm_topk, sel_l, w_l, threadIdx.x);
+  float *gs_l = reinterpret_cast<float *>(order + S);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // the sums of range r (groups [r GPW, r GPW + GPW) of K) of the token row, as expert_tile reads it
+  auto range_sums = [&](int r) {
+    const int G = a.K / kGroup, wg0 = min(r * GPW, G), wn = max(0, min(G, wg0 + GPW) - wg0);
+    const uint32_t xrange = wn > 0 ? (uint32_t)((a.x_rows - 1) * a.x_stride + wn * kGroup) * 2u : 0u;
+    row0_group_sums<GPW>(make_rsrc(a.x + (size_t)wg0 * kGroup, xrange), 16u * (uint32_t)(lane >> 4), wn, lane,
+                         gs_l + wg0);
+  };
+  if (wave == 0) topk_token<EPL>(logits, E, topk, norm_topk, sel_l, w_l, lane);
+  // ranges: wave v >= 1 takes range v - 1, the last wave also the last range; a lone wave
+  // takes its own range after routing
+  const int r_lo = wave == 0 ? (waves == 1 ? 0 : waves) : wave - 1;
+  const int r_hi = wave == 0 ? (waves == 1 ? 1 : waves) : (wave == waves - 1 ? waves : wave);
+  for (int r = r_lo; r < r_hi; ++r) range_sums(r);
   __syncthreads();
   // thread s ranks slot s's expert among the S distinct chosen experts
   const int s = threadIdx.x;
@@ -544,7 +564,7 @@ __global__ __launch_bounds__(1024) void moe_gate_up_one_token_kernel(MoeArgs a, 
   }
   __syncthreads();
   const int i = blockIdx.y;
-  expert_tile<GPW, SD, 0, true>(a, order[i], i, 1, lds);
+  expert_tile<GPW, SD, 0, true, true>(a, order[i], i, 1, lds, gs_l);
 }
 
 // tile_dot_lds for two blocks of 16 staged rows at once (xs: row 0 of the first block, the
@@ -1096,7 +1116,7 @@ template <int GPW, int SD, int EPL>
 static void launch_one_token_inst(const MoeArgs &a, const float *logits, int E, int topk, int norm_topk, int *sel,
                                   float *w, int *tok, int *inv, int *items, int *n_items, hipStream_t st) {
   const int waves = expert_waves(a.K), S = topk + 1;
-  const size_t lds = (size_t)(waves - 1) * 64 * 16 + (size_t)S * 12;
+  const size_t lds = (size_t)(waves - 1) * 64 * 16 + (size_t)S * 12 + (size_t)(a.K / kGroup) * 4;
   moe_gate_up_one_token_kernel<GPW, SD, EPL><<<dim3(a.tiles_per_expert, S), 64 * waves, lds, st>>>(
       a, logits, E, topk, norm_topk, sel, w, tok, inv, reinterpret_cast<int4 *>(items), n_items);
 }

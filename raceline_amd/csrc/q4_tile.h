@@ -240,9 +240,13 @@ __device__ __forceinline__ void book_step(f32x4 &acc, f32x4 &asum, const half8 (
 // live = false and read zeros. wn = real groups of the wave's part.
 // For native books the returned total already includes 0.5 * asum (kInt16); the row
 // scale is the caller's.
-template <int GPW, int SD, int BOOK = kAffine>
+// NACC: accumulator rows formed (1 when only token row 0 exists; its value is the same).
+// PRE (affine): gs0 holds the group sums of token row 0 for the wave's groups, formed
+// beforehand (row0_group_sums: the same two MFMAs, so the same bits), in place of forming
+// them here; only row 0's results are then valid (NACC = 1).
+template <int GPW, int SD, int BOOK = kAffine, int NACC = 4, bool PRE = false>
 __device__ __forceinline__ f32x4 tile_dot_rows(const WaveTile &w, __amdgpu_buffer_rsrc_t rx, uint32_t xoff, bool live,
-                                               int wn, int lane) {
+                                               int wn, int lane, const float *gs0 = nullptr) {
   u32x4 wq[GPW / 2], sq[GPW / 4];
   auto ldx = [&](int jg, int s) -> u32x4 {
     const bool ok = live && jg < wn;
@@ -265,7 +269,16 @@ __device__ __forceinline__ f32x4 tile_dot_rows(const WaveTile &w, __amdgpu_buffe
     }
     const half8 af[2] = {__builtin_bit_cast(half8, prep_act<BOOK>(ax[jg % 3][0])),
                          __builtin_bit_cast(half8, prep_act<BOOK>(ax[jg % 3][1]))};
-    book_step<GPW, SD, 4, BOOK>(acc, asum, af, wq, sq, jg);
+    if constexpr (BOOK == kAffine) {
+      if constexpr (PRE) {
+        const float g = jg < wn ? gs0[jg] : 0.0f;   // past the range: the zero sum of zero operands
+        group_step_gs<GPW, SD, NACC>(acc, af, f32x4{g, g, g, g}, wq, sq, jg);
+      } else {
+        group_step<GPW, SD, NACC>(acc, af, wq, sq, jg);
+      }
+    } else {
+      book_step<GPW, SD, NACC, BOOK>(acc, asum, af, wq, sq, jg);
+    }
     // The group's epilogue happens here, not after the last group: without this the
     // compiler sinks every group's scale/bias FMAs below the last MFMA and keeps all
     // the partial products alive (register spills).
@@ -276,6 +289,34 @@ __device__ __forceinline__ f32x4 tile_dot_rows(const WaveTile &w, __amdgpu_buffe
     for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(0.5f, asum[v], acc[v]);
   }
   return acc;
+}
+
+// The group sums of token row 0 for groups [0, wn) of a wave's part, as tile_dot_rows forms
+// them (the same operands and the same two MFMAs against ones), written to out[jg] by lane
+// 0. rx and xoff as for tile_dot_rows, with lane (c16, j4) live only for c16 = 0.
+template <int GPW>
+__device__ __forceinline__ void row0_group_sums(__amdgpu_buffer_rsrc_t rx, uint32_t xoff, int wn, int lane,
+                                                float *out) {
+  const bool live = (lane & 15) == 0;
+  constexpr int C = GPW < 8 ? GPW : 8;   // groups loaded at once (2 C operands in registers)
+#pragma unroll
+  for (int c0 = 0; c0 < GPW; c0 += C) {
+    u32x4 ax[C][2];
+#pragma unroll
+    for (int j = 0; j < C; ++j)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        ax[j][s] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rx, live && c0 + j < wn ? xoff + (uint32_t)((c0 + j) * kGroup + 32 * s) * 2u : kFarOffset, 0,
+                       0));
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const half8 af[2] = {__builtin_bit_cast(half8, prep_x8(ax[j][0])), __builtin_bit_cast(half8, prep_x8(ax[j][1]))};
+      const f32x4 gsv = group_sums(af);
+      if (lane == 0 && c0 + j < wn) out[c0 + j] = gsv[0];
+    }
+  }
 }
 
 // tile_dot_rows for two tiles at once (the same groups of two weight tiles, w0 and w1, one

@@ -19,8 +19,10 @@ layer at T=1 and T=512 (config 5), each projection's kernel time, the six-launch
 k, v as separate matrices), the native int15 MoE and linear, the 9B layer and the 27B
 prefill with bf16 scales (the .rlm files' scale type), the output head at a vocabulary of
 248,320, the engine's rl_mlp over .rlm files (dense 9B-shaped and the MoE layer) beside the
-sum of its parts, and the CPU baseline: the reference's numpy dequant + fp32 matmul
-(oracle.linear_affine_cpu_f32) on a bounded sample, timed on this host.
+sum of its parts, a streaming probe of what this box's HBM delivers to plain read and copy
+kernels (context for the roofline fractions, which stay against 8 TB/s), and the CPU
+baseline: the reference's numpy dequant + fp32 matmul (oracle.linear_affine_cpu_f32) on a
+bounded sample, timed on this host.
 
 Timing: each entry captures one HIP graph of exactly --steps consecutive steps over its
 rotating weight copies, replays it untimed (at least --warmup steps, and its first replay),
@@ -607,6 +609,64 @@ def bench_launch_cost(device, steps, warmup):
             "empty_launch_us": round(t_empty * 1e6, 2)}
 
 
+def bench_stream_probe(device, reps=8):
+    """What this box's HBM delivers to plain streaming kernels, as context for the roofline
+    fractions (which stay against 8 TB/s): a read stream (rlq_stream_read: 16-byte
+    non-temporal loads from every CU over 1 GiB, nothing written) and a copy stream
+    (torch.neg from one 1 GiB tensor into another), each `reps` times back to back in a
+    captured graph over two pairs of buffers (4 GiB in all, far past the 256 MB Infinity
+    Cache), replayed between two events."""
+    import torch
+
+    from raceline_amd import ops
+
+    n = 1 << 28                       # 1 GiB of fp32
+    bufs = [torch.ones(n, dtype=torch.float32, device=device) for _ in range(4)]
+    out = torch.zeros(1, dtype=torch.float32, device=device)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    def timed(fn, reps=reps):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            for i in range(2):
+                fn(i)                 # eager warm-up on the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(reps):
+                fn(i)
+        with torch.cuda.stream(stream):
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+    t_read = timed(lambda i: ops.lib.call("rlq_stream_read", bufs[i % 2].data_ptr(), 4 * n, out.data_ptr(),
+                                          ops._stream()))
+    t_copy = timed(lambda i: torch.neg(bufs[i % 2], out=bufs[2 + i % 2]))
+    # the same read stream at the headline kernel's size (the 9B gate_up's algorithmic bytes
+    # at M = 1), each launch on the next slice of the 4 GiB, as the decode launches rotate
+    small = 56729600 // 256 * 256
+    slices = [(b, o) for b in range(4) for o in range(0, 4 * n - small + 1, small)]
+    t_small = timed(lambda i: ops.lib.call("rlq_stream_read", bufs[slices[i % len(slices)][0]].data_ptr() +
+                                           slices[i % len(slices)][1], small, out.data_ptr(), ops._stream()),
+                    reps=len(slices))
+    res = {"read_GBps": round(4 * n / t_read / 1e9, 1), "copy_GBps": round(8 * n / t_copy / 1e9, 1),
+           "bytes_read": 4 * n, "read_56.7MB_us": round(t_small * 1e6, 2),
+           "read_56.7MB_GBps": round(small / t_small / 1e9, 1),
+           "kernels": "rlq_stream_read (read) and torch.neg (copy) of 1 GiB, and rlq_stream_read of 56.7 MB "
+                      "slices of 4 GiB, graph-timed"}
+    log(f"[bench] HBM stream probe: read {res['read_GBps']} GB/s, copy {res['copy_GBps']} GB/s, "
+        f"56.7 MB reads {res['read_56.7MB_us']} us each ({res['read_56.7MB_GBps']} GB/s)")
+    del bufs
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_part(part, steps, warmup):
     import torch
 
@@ -620,6 +680,8 @@ def bench_part(part, steps, warmup):
 
         with tempfile.TemporaryDirectory() as tmp:
             return bench_engine(dev, steps, warmup, tmp)
+    if part == "stream":
+        return bench_stream_probe(dev)
     fn = {"prefill": bench_prefill, "moe": bench_moe, "decode": bench_decode, "epilogue": bench_native_epilogue,
           "launch": bench_launch_cost, "bf16": bench_bf16, "head": bench_head}[part]
     return fn(dev, steps, warmup)
@@ -925,7 +987,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no detail configs, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--part", choices=["prefill", "moe", "decode", "epilogue", "launch", "bf16", "head", "engine",
-                                       "cpu"],
+                                       "stream", "cpu"],
                     help="run only this part of the detail (for rocprofv3); prints its figures as JSON")
     ap.add_argument("--profile", nargs="?", const="gemv", choices=["gemv", "moe", "gemm"],
                     help="launch only the dominant kernel (gemv), the MoE layer at T=512 (moe) or the prefill "
@@ -1010,6 +1072,7 @@ def main():
                                               "GB/s": round(layer_bytes(CFG2_9B, 1) / t6 / 1e9, 1)}
         del r6, l6
         torch.cuda.empty_cache()
+        detail["hbm_stream_probe"] = bench_stream_probe(dev)
 
         c27 = copies_for(CFG3_27B)
         log(f"[bench] building {c27} copies of the 27B layer")

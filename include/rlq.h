@@ -168,6 +168,14 @@ int rlq_group_sums(const void *x, int x_stride, int M, int K, float *gsum, void 
  * entry point: the matmuls never materialise W. */
 int rlq_dequant_affine(const void *packed, int scale_dtype, int K, int N, float *out, void *stream);
 
+/* Reads `bytes` bytes of device memory at p as a plain stream (16-byte non-temporal loads from
+ * every CU, nothing else), the read rate this device gives a kernel that only streams: the
+ * context for the decode kernels' fraction of the 8 TB/s peak. out (one float) is written only
+ * for data no real buffer holds. p 16-byte aligned, bytes a multiple of 16. A measurement
+ * helper with no counterpart in the reference (its bench/hw/gpu_probe.py:33-103 plays this
+ * part on Apple GPUs). */
+int rlq_stream_read(const void *p, size_t bytes, float *out, void *stream);
+
 /* ---------------------------------------------------------------- mixture of experts */
 
 /* A MoE MLP of E routed experts plus one shared expert (number E), each a gate/up matrix

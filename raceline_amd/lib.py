@@ -37,6 +37,7 @@ SIGNATURES = {
                                          c_int, c_int, c_void_p, c_size_t, c_void_p]),
     "rlq_group_sums": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
     "rlq_dequant_affine": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "rlq_stream_read": (c_int, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "rlq_packed_codes_bytes": (c_size_t, [c_int, c_int]),
     "rlq_pack_codes": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "rlq_pack_native_blocked": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),

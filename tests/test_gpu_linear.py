@@ -334,6 +334,25 @@ def test_group_sums(gpu):
     np.testing.assert_array_equal(got.cpu().numpy(), ref)
 
 
+def test_stream_read_probe(gpu):
+    """rlq_stream_read (the bench's read-rate probe) streams a buffer, ragged sizes included,
+    without writing its output for ordinary data, and refuses misaligned arguments."""
+    import torch
+
+    from raceline_amd import lib, ops
+
+    buf = torch.arange(1 << 20, dtype=torch.int32, device=gpu)
+    out = torch.full((1,), -2.0, dtype=torch.float32, device=gpu)
+    for nbytes in (0, 16, 4096 + 48, buf.numel() * 4):
+        assert lib.call("rlq_stream_read", buf.data_ptr(), nbytes, out.data_ptr(), ops._stream()) == 0
+    torch.cuda.synchronize()
+    assert out.item() == -2.0
+    with pytest.raises(lib.RlqError):
+        lib.call("rlq_stream_read", buf.data_ptr() + 4, 64, out.data_ptr(), ops._stream())
+    with pytest.raises(lib.RlqError):
+        lib.call("rlq_stream_read", buf.data_ptr(), 40, out.data_ptr(), ops._stream())
+
+
 @pytest.mark.parametrize("M,K,N", O.REFERENCE_TEST_CASES)
 def test_reference_correctness_cases(gpu, M, K, N):
     """The reference's own correctness cases (tests/test_linear.mm:440-446): layers drawn

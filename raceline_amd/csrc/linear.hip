@@ -492,6 +492,99 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
   }
 }
 
+// One token, two adjacent tiles per workgroup (t0 = 2 * block, t1 = t0 + 1; affine, no K
+// split): each wave stages its activation range once, issues both tiles' weight loads at
+// once, and forms each group's sums once for both tiles. A weight of many tiles then takes
+// half as many workgroups, each with twice the loads in flight. Each tile's products, sums
+// and cross-wave order are gemv_q4a_kernel<1>'s, so the bits are the same.
+// Held to 80 VGPRs (six waves per SIMD): three 8-wave workgroups then share a CU, 768 at
+// once on the chip.
+template <int GPW, int SD, bool ACC>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void gemv_q4a_m1_pair_kernel(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int waves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, j4 = lane >> 4;
+  const int G = a.K / kGroup, G4 = quads_of(a.K);
+  const int tiles = tiles_of(a.N);
+  const int t0 = 2 * blockIdx.x, t1 = t0 + 1;
+  f32x4 *red0 = reinterpret_cast<f32x4 *>(lds), *red1 = red0 + (size_t)(waves - 1) * 64;   // [waves-1][64] each
+
+  const int wg0 = wave * GPW;
+  const int wn = max(0, min(G, wg0 + GPW) - wg0);
+  const int wl = wn > 0 ? min(GPW, (wn + 3) / 4 * 4) : 0;
+  const WaveTile w0 = wave_tile(a.codes, a.sb, t0, G4, wg0, wl);
+  const WaveTile w1 = wave_tile(a.codes, a.sb, min(t1, tiles - 1), G4, wg0, t1 < tiles ? wl : 0);
+  const uint32_t xrange = wn > 0 ? (uint32_t)(wn * kGroup) * 2u : 0u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (size_t)min(wg0, G) * kGroup, xrange);
+
+  // as gemv_q4a_kernel<1>: the activation row first, then every weight load, the row staged
+  // in LDS in operand order while the weights are in flight
+  constexpr int XCH = GPW * 8;
+  constexpr int XPER = (XCH + 63) / 64;
+  _Float16 *xs = reinterpret_cast<_Float16 *>(lds + (size_t)2 * (waves - 1) * 64 * 16) + (size_t)wave * GPW * kGroup;
+  u32x4 xr[XPER], wq0[GPW / 2], sq0[GPW / 4], wq1[GPW / 2], sq1[GPW / 4];
+#pragma unroll
+  for (int i = 0; i < XPER; ++i) {
+    const int chunk = lane + 64 * i;
+    const bool in_range = chunk < XCH && (chunk >> 3) < wn;
+    xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, in_range ? 16u * chunk : kFarOffset, 0, 0));
+  }
+  issue_tile_loads<GPW, kAffine>(w0, lane, wq0, sq0);
+  issue_tile_loads<GPW, kAffine>(w1, lane, wq1, sq1);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < XPER; ++i) {
+    const int chunk = lane + 64 * i;
+    if (chunk < XCH) *reinterpret_cast<u32x4 *>(xs + 8 * chunk) = prep_x8(xr[i]);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const _Float16 *xa = xs + 8 * j4;
+  half8 an[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) an[s] = *reinterpret_cast<const half8 *>(xa + 32 * s);
+  f32x4 acc0 = {}, acc1 = {};
+#pragma unroll
+  for (int jg = 0; jg < GPW; ++jg) {
+    const half8 af[2] = {an[0], an[1]};
+    if (jg + 1 < GPW) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) an[s] = *reinterpret_cast<const half8 *>(xa + (jg + 1) * kGroup + 32 * s);
+    }
+    const f32x4 gsv = group_sums(af);
+    group_step_gs<GPW, SD, 1>(acc0, af, gsv, wq0, sq0, jg);
+    group_step_gs<GPW, SD, 1>(acc1, af, gsv, wq1, sq1, jg);
+  }
+
+  // the waves' partials meet in wave order, as in reduce_waves
+  if (wave > 0) {
+    red0[(wave - 1) * 64 + lane] = acc0;
+    red1[(wave - 1) * 64 + lane] = acc1;
+  }
+  __syncthreads();
+  if (wave != 0 || j4 != 0) return;
+  for (int w = 1; w < waves; ++w) {
+    const f32x4 o0 = red0[(w - 1) * 64 + lane], o1 = red1[(w - 1) * 64 + lane];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      acc0[v] += o0[v];
+      acc1[v] += o1[v];
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int n = 16 * (t0 + h) + c16;
+    if (n < a.N) {
+      float *dst = a.y + n;
+      const float val = h ? acc1[0] : acc0[0];
+      *dst = ACC ? *dst + val : val;
+    }
+  }
+}
+
 // the partials of a split weight (the counters sit in the workspace's first kGemvCountBytes)
 static size_t gemv_workspace(int M, int K, int N) {
   const int S = split_of(K, N);
@@ -548,6 +641,24 @@ static bool pair_tiles(int M, int K, int N) {
   return (long long)tiles_of(N) * S >= 1024 || (long long)M * (S == 1 ? K : gsplit_of(K, S) * kGroup) > 24576;
 }
 
+// One token on a weight of at least this many tiles (and no K split) takes two tiles per
+// workgroup (gemv_q4a_m1_pair_kernel): the output head (15520 tiles, about 15 rounds of
+// the chip with one tile per workgroup) pays each workgroup's start (staging the row, the
+// reduction, the stores) half as often: 248320 x 4096 at M = 1 100.5-105.7 -> 92.4-94.5
+// us. Below it one tile per workgroup stays: the 9B gate_up (1536 tiles) measured the same
+// or slightly slower paired (11.3-12.1 against 11.6-11.7 us), the 27B gate_up (2176
+// tiles) 1 us slower alone.
+constexpr int kM1PairTiles = 4096;
+
+template <int SD, bool ACC>
+static int launch_m1_pair(int tiles, int threads, size_t lds, hipStream_t st, const GemvArgs &a) {
+  static LdsOptIn lds_opt;
+  if (int rc = allow_large_lds(reinterpret_cast<const void *>(&gemv_q4a_m1_pair_kernel<8, SD, ACC>), lds_opt))
+    return rc;
+  gemv_q4a_m1_pair_kernel<8, SD, ACC><<<(tiles + 1) / 2, threads, lds, st>>>(a);
+  return 0;
+}
+
 static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes, const void *sbq,
                     int sd, const float *srow, float *y, int y_stride, int accum, int *cnt, float *part,
                     size_t part_bytes, hipStream_t st) {
@@ -575,7 +686,13 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
   const dim3 grid(tiles_of(N), S);
   const int threads = 64 * waves;
   int rc;
-  if (M == 1) rc = gpw == 8    ? launch_gemv<1, 8>(book, sd, accum, grid, threads, lds, st, a)
+  if (M == 1 && gpw == 8 && S == 1 && book == kAffine && tiles_of(N) >= kM1PairTiles) {
+    const size_t lds2 = (size_t)2 * (waves - 1) * 64 * 16 + (size_t)waves * gpw * kGroup * 2;
+    rc = sd == RLQ_BF16 ? (accum ? launch_m1_pair<1, true>(tiles_of(N), threads, lds2, st, a)
+                                 : launch_m1_pair<1, false>(tiles_of(N), threads, lds2, st, a))
+                        : (accum ? launch_m1_pair<0, true>(tiles_of(N), threads, lds2, st, a)
+                                 : launch_m1_pair<0, false>(tiles_of(N), threads, lds2, st, a));
+  } else if (M == 1) rc = gpw == 8    ? launch_gemv<1, 8>(book, sd, accum, grid, threads, lds, st, a)
                    : gpw == 12 ? launch_gemv<1, 12>(book, sd, accum, grid, threads, lds, st, a)
                    : gpw == 16 ? launch_gemv<1, 16>(book, sd, accum, grid, threads, lds, st, a)
                                : launch_gemv<1, 24>(book, sd, accum, grid, threads, lds, st, a);

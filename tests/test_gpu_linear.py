@@ -127,6 +127,25 @@ def test_rows_do_not_depend_on_other_rows(gpu, K):
         np.testing.assert_array_equal(y_one[0], y_all[m])
 
 
+@pytest.mark.parametrize("K,N,sd", [(1024, 65552, "bf16"), (512, 65536 + 160, "f16")])
+def test_one_token_two_tiles_per_workgroup(gpu, K, N, sd):
+    """One token on a weight of 4096 tiles or more runs two tiles per workgroup (an odd tile
+    count leaves the last workgroup one tile): the row is within the bar of the fp64 product,
+    bit-identical to the same row inside a 2-row call (one tile per workgroup), and ACCUM
+    adds to y."""
+    q, s, b = make_layer(K + 5, N, K, sd)
+    x = make_x(K + 6, 2, K)
+    wt = upload(q, s, b, sd, gpu)
+    y1 = _run(gpu, x[:1], wt, kernel=1)
+    y2 = _run(gpu, x, wt, kernel=1)
+    np.testing.assert_array_equal(y1[0], y2[0])
+    cols = sample_cols(N, seed=K)
+    O.check_close(y1[:, cols], O.linear_affine_f64(x[:1], q[cols], s[cols], b[cols], sd), TOL, f"K={K} N={N}")
+    y0 = np.random.default_rng(K + 1).standard_normal((1, N)).astype(np.float32)
+    ya = _run(gpu, x[:1], wt, kernel=1, accum_into=y0)
+    np.testing.assert_array_equal(ya, y0 + y1)
+
+
 @pytest.mark.parametrize("K,N", [(2048, 640), (8192, 1024)])   # the second splits K
 def test_gemm_rows_do_not_depend_on_other_rows(gpu, K, N):
     """The prefill kernel keeps the same rule: rows 50..119 alone (M = 70) give the same

@@ -651,10 +651,22 @@ int rl_mlp(rl_engine *e, int layer, float *h, int h_stride, int T, void *stream)
                 2 * I);
     RLQ_REQUIRE(dn->q->k == I && dn->q->n == c.hidden && gu->q->k == c.hidden, "layer %d: MLP shapes do not match",
                 layer);
-    float *proj = e->proj.as<float>();
-    if (int rc = linear_rows(e, *gu, 0, 2 * I, xn, e->x_stride, T, proj, e->proj_stride, 0, st)) return rc;
     const float *cs = dn->q->native ? dn->col.as<float>() : nullptr;
-    if (int rc = rlq_moe_swiglu(proj, e->proj_stride, T, I, cs, e->act.p, e->act_stride, st)) return rc;
+    // decode sizes of an affine gate/up: the SwiGLU fused into the gate/up launch (the same
+    // bits as the two steps below)
+    int fused = 1;
+    if (gu->q->kind == kKindQ4a && !cs && T <= 8) {
+      const char *codes = gu->packed.as<char>();
+      fused = linear_swiglu_packed(xn, e->x_stride, T, gu->q->k, I, codes,
+                                   codes + packed_code_bytes(gu->q->k, gu->q->n_pad), RLQ_BF16,
+                                   e->act.as<_Float16>(), e->act_stride, st);
+      if (fused < 0) return fused;
+    }
+    if (fused) {
+      float *proj = e->proj.as<float>();
+      if (int rc = linear_rows(e, *gu, 0, 2 * I, xn, e->x_stride, T, proj, e->proj_stride, 0, st)) return rc;
+      if (int rc = rlq_moe_swiglu(proj, e->proj_stride, T, I, cs, e->act.p, e->act_stride, st)) return rc;
+    }
     return linear_rows(e, *dn, 0, c.hidden, e->act.as<_Float16>(), e->act_stride, T, h, h_stride, 1, st);
   }
   // encode_moe (src/engine.mm:965-1059)

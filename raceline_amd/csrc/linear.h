@@ -21,4 +21,12 @@ int linear_packed(int kernel, int book, const _Float16 *x, int x_stride, int M, 
                   const void *sbq, int sd, const float *srow, float *y, int y_stride, int accum, void *ws,
                   size_t ws_bytes, hipStream_t st);
 
+// A dense MLP's gate/up product with the SwiGLU fused, for an affine packed matrix of 2I
+// rows (gate rows [0, I), up rows [I, 2I)): act[m][i] = half(silu(g[m][i]) * u[m][i]) with
+// g, u the rows of x W^T, the same bits as linear_packed followed by the SwiGLU kernel.
+// For the decode sizes (M <= 8) whose K the decode kernel covers with 8 groups per wave
+// and no K split; returns 1 (nothing launched) for other shapes, 0 when launched.
+int linear_swiglu_packed(const _Float16 *x, int x_stride, int M, int K, int I, const void *codes, const void *sbq,
+                         int sd, _Float16 *act, int act_stride, hipStream_t st);
+
 }  // namespace rlq

@@ -207,6 +207,10 @@ struct GemvArgs {
   int split, gsplit;    // K split: S workgroups per tile, gsplit groups each (S = 1: none)
   float *part;          // S > 1: partial sums [S][M][N]
   int *cnt;             // S > 1: arrivals per tile (zero between calls)
+  // SWIGLU kernels: tile t (gate rows) pairs with tile t + up_off (the matching up rows),
+  // and act[m][n] = half(silu(gate) * up) replaces y
+  int up_off, act_stride;
+  _Float16 *act;
 };
 
 // The workspace's first kGemvCountBytes hold the split counters (zero before the first
@@ -425,7 +429,11 @@ __global__ __launch_bounds__(1024) void gemv_q4a_kernel(GemvArgs a) {
 // no group waits on an L2 read. Taken where a wave holds 8 groups: two tiles' loads then
 // fit the registers one tile of 16 groups takes. Each tile's sums are the one-tile
 // kernel's, in the same order, so the results do not depend on the pairing.
-template <int GPW, int SD, bool ACC, int BOOK>
+// SWIGLU (affine, no K split): the workgroup's tiles are gate tile t0 = block and up tile
+// t1 = t0 + up_off, and it writes act = half(silu(gate) * up) for its 16 features instead
+// of y (the gate/up product of a dense MLP with the SwiGLU fused; each tile's sums are the
+// same, so act has the bits of the linear followed by moe_swiglu_kernel).
+template <int GPW, int SD, bool ACC, int BOOK, bool SWIGLU = false>
 __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int waves = blockDim.x >> 6;
@@ -434,7 +442,7 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
   const int c16 = lane & 15, j4 = lane >> 4;
   const int G = a.K / kGroup, G4 = quads_of(a.K);
   const int tiles = tiles_of(a.N);
-  const int t0 = 2 * blockIdx.x, t1 = t0 + 1;
+  const int t0 = SWIGLU ? (int)blockIdx.x : 2 * blockIdx.x, t1 = SWIGLU ? t0 + a.up_off : t0 + 1;
   const int M = a.M;
 
   const int g_lo = blockIdx.y * a.gsplit, g_hi = min(G, g_lo + a.gsplit);   // the split's groups
@@ -466,6 +474,15 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
       acc0[v] += o0[v];
       acc1[v] += o1[v];
     }
+  }
+  if constexpr (SWIGLU) {
+    const int n = 16 * t0 + c16;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * j4 + v;
+      if (m < M) a.act[(size_t)m * a.act_stride + n] = swiglu_half(acc0[v], acc1[v]);
+    }
+    return;
   }
   if (a.split > 1) {
     f32x4 accs[2] = {acc0, acc1};
@@ -499,7 +516,8 @@ __global__ __launch_bounds__(1024) void gemv_q4a_pair_kernel(GemvArgs a) {
 // and cross-wave order are gemv_q4a_kernel<1>'s, so the bits are the same.
 // Held to 80 VGPRs (six waves per SIMD): three 8-wave workgroups then share a CU, 768 at
 // once on the chip.
-template <int GPW, int SD, bool ACC>
+// SWIGLU: as gemv_q4a_pair_kernel's (gate tile t0 = block, up tile t0 + up_off, act out).
+template <int GPW, int SD, bool ACC, bool SWIGLU = false>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void gemv_q4a_m1_pair_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int waves = blockDim.x >> 6;
@@ -508,7 +526,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
   const int c16 = lane & 15, j4 = lane >> 4;
   const int G = a.K / kGroup, G4 = quads_of(a.K);
   const int tiles = tiles_of(a.N);
-  const int t0 = 2 * blockIdx.x, t1 = t0 + 1;
+  const int t0 = SWIGLU ? (int)blockIdx.x : 2 * blockIdx.x, t1 = SWIGLU ? t0 + a.up_off : t0 + 1;
   f32x4 *red0 = reinterpret_cast<f32x4 *>(lds), *red1 = red0 + (size_t)(waves - 1) * 64;   // [waves-1][64] each
 
   const int wg0 = wave * GPW;
@@ -573,6 +591,10 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
       acc0[v] += o0[v];
       acc1[v] += o1[v];
     }
+  }
+  if constexpr (SWIGLU) {
+    a.act[16 * t0 + c16] = swiglu_half(acc0[0], acc1[0]);
+    return;
   }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -705,6 +727,41 @@ static int run_gemv(int book, const _Float16 *x, int x_stride, int M, int K, int
   if (rc) return rc;
   RLQ_HIP(hipGetLastError());
   return 0;
+}
+
+template <int SD>
+static int launch_swiglu(int M, int I, int waves, const GemvArgs &a, hipStream_t st) {
+  static LdsOptIn lds1, lds2;
+  if (M == 1) {
+    const void *fn = reinterpret_cast<const void *>(&gemv_q4a_m1_pair_kernel<8, SD, false, true>);
+    if (int rc = allow_large_lds(fn, lds1)) return rc;
+    const size_t lds = (size_t)2 * (waves - 1) * 64 * 16 + (size_t)waves * 8 * kGroup * 2;
+    gemv_q4a_m1_pair_kernel<8, SD, false, true><<<I / 16, 64 * waves, lds, st>>>(a);
+  } else {
+    const void *fn = reinterpret_cast<const void *>(&gemv_q4a_pair_kernel<8, SD, false, kAffine, true>);
+    if (int rc = allow_large_lds(fn, lds2)) return rc;
+    gemv_q4a_pair_kernel<8, SD, false, kAffine, true><<<I / 16, 64 * waves, gemv_lds_bytes(M, waves, 8), st>>>(a);
+  }
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+int linear_swiglu_packed(const _Float16 *x, int x_stride, int M, int K, int I, const void *codes, const void *sbq,
+                         int sd, _Float16 *act, int act_stride, hipStream_t st) {
+  if (M < 1 || M > kGemvMaxM || I < 16 || I % 16 || gemv_gpw(K) != 8 || gemv_waves(K) > 16 || split_of(K, 2 * I) != 1)
+    return 1;
+  GemvArgs a = {};
+  a.x = x;
+  a.codes = static_cast<const u32x4 *>(codes);
+  a.sb = static_cast<const u32x4 *>(sbq);
+  a.x_stride = x_stride; a.M = M; a.K = K; a.N = 2 * I;
+  a.split = 1;
+  a.gsplit = K / kGroup;
+  a.up_off = I / 16;
+  a.act = act;
+  a.act_stride = act_stride;
+  const int waves = gemv_waves(K);
+  return sd == RLQ_BF16 ? launch_swiglu<1>(M, I, waves, a, st) : launch_swiglu<0>(M, I, waves, a, st);
 }
 
 int linear_packed(int kernel, int book, const _Float16 *x, int x_stride, int M, int K, int N, const void *codes,

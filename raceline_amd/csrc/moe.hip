@@ -438,7 +438,6 @@ __device__ __forceinline__ int4 clamp_item(int4 it, int n_experts, int n_rows) {
 // The token of sorted row r, clamped to the call's tokens (see clamp_item).
 __device__ __forceinline__ int token_of(const int *tok, int r, int T) { return min(max(tok[r], 0), T - 1); }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
 // One item's products for one 16-row weight tile (tile = blockIdx.x) by all the workgroup's
 // waves, each a range of GPW groups of K; the waves meet in LDS in wave order and wave 0

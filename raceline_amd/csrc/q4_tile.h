@@ -101,6 +101,20 @@ __device__ __forceinline__ u32x4 prep_x8(u32x4 p) {
   return r;
 }
 
+// SwiGLU's gate activation, silu(v) = v / (1 + e^-v) (kernels/ops.metal:446-455); one
+// definition for every kernel that applies it, so that they give the same bits
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// half(silu(g) * u) with the product rounded to fp32 and then to fp16, as the SwiGLU kernel
+// over fp32 gate/up rows computes it (moe_swiglu_kernel). The barrier keeps the compiler
+// from fusing the multiply into the conversion (v_fma_mix rounds once, which can differ in
+// the last bit), so a kernel with the SwiGLU fused gives that kernel's bits.
+__device__ __forceinline__ _Float16 swiglu_half(float g, float u) {
+  float p = silu(g) * u;
+  asm volatile("" : "+v"(p));
+  return static_cast<_Float16>(p);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kBufFlags);
 }

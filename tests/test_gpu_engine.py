@@ -137,6 +137,33 @@ def test_dense_mlp(gpu, tmp_path, book):
                 assert torch.equal(sub, h[lo:T] if T > 8 else h[T - 1:T])
 
 
+@pytest.mark.parametrize("hidden,inter", [(256, 512), (4096, 1024), (320, 768)])
+def test_dense_mlp_same_bits_as_its_steps(gpu, tmp_path, hidden, inter):
+    """rl_mlp on an affine dense MLP at decode sizes fuses the SwiGLU into the gate/up launch;
+    its result must be the bits of the steps run one by one: rl_norm, rl_linear on gate_up,
+    the SwiGLU kernel (rlq_moe_swiglu), rl_linear on down with ACCUM."""
+    import torch
+
+    from raceline_amd import ops
+
+    m = MF.write_dense_model(str(tmp_path / "m.rlm"), seed=hidden + inter, hidden=hidden, intermediate=inter,
+                             layers=2)
+    with Engine(m.path, max_chunk=16) as e:
+        for T in (1, 3, 8, 9):
+            h0 = np.random.default_rng(T + hidden).standard_normal((T, hidden)).astype(np.float32)
+            h = to_dev(h0, gpu)
+            e.mlp(1, h)
+            hs = to_dev(h0, gpu)
+            xn = e.norm(1, 1, hs)
+            g = e.linear("layers.1.mlp.gate_up", xn, n=2 * inter)
+            act = torch.empty((T, inter), dtype=torch.float16, device=gpu)
+            ops.lib.call("rlq_moe_swiglu", g.data_ptr(), g.stride(0), T, inter, None, act.data_ptr(), act.stride(0),
+                         ops._stream())
+            e.linear("layers.1.mlp.down", act, out=hs, accum=True)
+            _sync()
+            assert torch.equal(h, hs), f"T={T} H={hidden} I={inter}"
+
+
 def _moe_ref(m, layer, h0):
     cfg = m.cfg
     E, topk, I, H = cfg["num_experts"], cfg["num_experts_per_tok"], cfg["moe_intermediate_size"], cfg["hidden_size"]

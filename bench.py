@@ -899,6 +899,39 @@ def profile_dominant(launches):
         f"calibration: 10 x torch.neg over {CALIBRATION_BYTES >> 20} MiB")
 
 
+def profile_gemv8(launches):
+    """--profile gemv8: the 27B gate_up (K = 5120, N = 34816) at M = 1 and at M = 8 (the MTP
+    draft regime), launched eagerly in turn over rotating weight copies (the one-tile kernel
+    at M = 1, the two-tile kernel with rows staged in LDS at M = 8), then the calibration
+    kernel of profile_dominant. Meant to run under rocprofv3 --pmc: the two kernels' counters
+    compare the same weights' traffic at one and eight tokens."""
+    import torch
+
+    from raceline_amd import lib, ops, synth
+    from raceline_amd.configs import CFG3_27B
+
+    lib.load()
+    dev = torch.device("cuda:0")
+    _, K, N = [c for c in CFG3_27B if c[0] == "gate_up"][0]
+    copies = copies_for([("gate_up", K, N)])
+    ws = [synth.random_affine(N, K, 5 + 1000 * c, dev) for c in range(copies)]
+    xs = {M: synth.random_activations(M, K, 90 + M, dev) for M in (1, 8)}
+    ys = {M: torch.empty((M, N), dtype=torch.float32, device=dev) for M in (1, 8)}
+    for M in (1, 8):
+        ops._WS.get(dev, ops.workspace_bytes(M, K, N))
+    for i in range(launches):
+        for M in (1, 8):
+            ops.linear(xs[M], ws[i % copies], out=ys[M])
+    torch.cuda.synchronize()
+    a = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(10):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    log(f"[profile] gemv_q4a K={K} N={N} M=1 and M=8: {launches} launches each over {copies} copies; "
+        f"calibration: 10 x torch.neg over {CALIBRATION_BYTES >> 20} MiB")
+
+
 def profile_moe(launches, T=512):
     """--profile moe: the MoE layer (H=2048, E=256 + shared, I=512, top-8) at T tokens,
     launched eagerly over rotating copies of the experts (each step routes, multiplies and
@@ -989,9 +1022,10 @@ def main():
     ap.add_argument("--part", choices=["prefill", "moe", "decode", "epilogue", "launch", "bf16", "head", "engine",
                                        "stream", "cpu"],
                     help="run only this part of the detail (for rocprofv3); prints its figures as JSON")
-    ap.add_argument("--profile", nargs="?", const="gemv", choices=["gemv", "moe", "gemm"],
-                    help="launch only the dominant kernel (gemv), the MoE layer at T=512 (moe) or the prefill "
-                         "kernel on the 27B gate_up (gemm), eagerly, and a calibration kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--profile", nargs="?", const="gemv", choices=["gemv", "gemv8", "moe", "gemm"],
+                    help="launch only the dominant kernel (gemv), the 27B gate_up at M=1 and M=8 (gemv8), the MoE "
+                         "layer at T=512 (moe) or the prefill kernel on the 27B gate_up (gemm), eagerly, and a "
+                         "calibration kernel (for rocprofv3 --pmc)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -1002,6 +1036,9 @@ def main():
 
     if args.profile == "gemv":
         profile_dominant(max(args.steps, 40))
+        return
+    if args.profile == "gemv8":
+        profile_gemv8(max(args.steps, 20))
         return
     if args.profile == "moe":
         profile_moe(max(args.steps, 20))

@@ -26,7 +26,8 @@ bounded sample, timed on this host.
 
 Timing: each entry captures one HIP graph of exactly --steps consecutive steps over its
 rotating weight copies, replays it untimed (at least --warmup steps, and its first replay),
-then times one replay with HIP events on the stream it runs on.
+then times one replay with HIP events on the stream it runs on, queued directly behind one
+more untimed replay so that the GPU does not idle before it.
 """
 
 from __future__ import annotations
@@ -124,23 +125,35 @@ class LayerRunner(StepGraphs):
             ops.linear(self.xs[K], wt, out=self.ys[i], kernel=self.kernel)
 
 
-def time_steps(runner, steps, warmup):
-    """Seconds per step: one captured graph of exactly `steps` consecutive steps, replayed
-    max(1, ceil(warmup / steps)) times untimed (at least `warmup` steps, and the graph's first
-    replay, which costs more than later ones), then once between two events on its stream."""
-    torch = runner.torch
-    g = runner.graph_of(steps)
-    with torch.cuda.stream(runner.stream):
-        for _ in range(max(1, -(-warmup // steps))):
+def timed_replay(g, stream, warm=1):
+    """Seconds for one replay of the captured graph g on `stream`: `warm` untimed replays and
+    a host synchronization, then one more untimed replay and, right behind it on the stream,
+    the timed replay between two events, so that the GPU runs the timed replay with no idle
+    gap before it (a short graph timed right after the host's synchronization ran at lower
+    clocks: the 2 us norm of the engine entries read 4.9 us in graphs of 20 steps)."""
+    import torch
+
+    with torch.cuda.stream(stream):
+        for _ in range(warm):
             g.replay()
         torch.cuda.synchronize()
+        g.replay()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         g.replay()
         end.record()
         torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3
+
+
+def time_steps(runner, steps, warmup):
+    """Seconds per step: one captured graph of exactly `steps` consecutive steps, replayed
+    max(1, ceil(warmup / steps)) times untimed (at least `warmup` steps, and the graph's first
+    replay, which costs more than later ones), then timed (timed_replay)."""
+    g = runner.graph_of(steps)
+    t = timed_replay(g, runner.stream, max(1, -(-warmup // steps)))
     del g
-    return start.elapsed_time(end) / 1e3 / steps      # seconds per step
+    return t / steps      # seconds per step
 
 
 MOE_EXPERT_BYTES = 1769472   # codes + fp16 s/b of one expert's gate_up [1024][2048] and down [2048][512]
@@ -592,15 +605,7 @@ def bench_launch_cost(device, steps, warmup):
     with torch.cuda.graph(g, stream=stream):
         for _ in range(256):
             one.fill_(1.0)
-    with torch.cuda.stream(stream):
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-    t_empty = e0.elapsed_time(e1) / 1e3 / 256
+    t_empty = timed_replay(g, stream) / 256
     log(f"[bench] fit over N >= 4096: t0 = {t0 * 1e6:.2f} us per launch, stream rate {1 / slope / 1e9:.0f} GB/s; "
         f"fill of one float: {t_empty * 1e6:.2f} us per launch")
     return {"K": K, "points": [{"N": N, "bytes": b, "us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
@@ -635,15 +640,7 @@ def bench_stream_probe(device, reps=8):
         with torch.cuda.graph(g, stream=stream):
             for i in range(reps):
                 fn(i)
-        with torch.cuda.stream(stream):
-            g.replay()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            g.replay()
-            e1.record()
-            torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / 1e3 / reps
+        return timed_replay(g, stream) / reps
 
     t_read = timed(lambda i: ops.lib.call("rlq_stream_read", bufs[i % 2].data_ptr(), 4 * n, out.data_ptr(),
                                           ops._stream()))
@@ -709,15 +706,7 @@ def time_kernel(layers, shapes, M, idx, device, launches, kernel=0, outliers=0.0
     with torch.cuda.graph(g, stream=stream):
         for i in range(launches):
             ops.linear(x, layers[i % len(layers)][idx], out=y, kernel=kernel)
-    with torch.cuda.stream(stream):
-        g.replay()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        g.replay()
-        end.record()
-        torch.cuda.synchronize()
-    return start.elapsed_time(end) / 1e3 / launches
+    return timed_replay(g, stream) / launches
 
 
 def cpu_model() -> str:

@@ -90,6 +90,10 @@ __device__ __forceinline__ float norm_total(float ss, float *part) {
   return total;
 }
 
+// One element of a normed row, half(x * inv * w): the one expression every kernel that
+// norms a row uses, so that they give the same bits.
+__device__ __forceinline__ _Float16 norm_out(float x, float inv, float w) { return static_cast<_Float16>(x * inv * w); }
+
 // out[r][i] = half(h[r][i] * inv * w[i]), inv = 1 / sqrt(sum_i h[r][i]^2 / D + eps): one
 // workgroup per row. Each thread sums its elements i = tid, tid + 256, ... in order, and
 // the threads' sums meet in norm_total's tree, so a row's result depends on nothing but the
@@ -122,13 +126,97 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *h, 
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int i = threadIdx.x + j * kNormThreads;
-      if (i < D) o[i] = static_cast<_Float16>(xv[j] * inv * wv[j]);
+      if (i < D) o[i] = norm_out(xv[j], inv, wv[j]);
     }
   } else {
     for (int i = threadIdx.x; i < D; i += kNormThreads) ss = __builtin_fmaf(x[i], x[i], ss);
     const float inv = 1.0f / __builtin_sqrtf(norm_total(ss, part) / (float)D + eps);
-    for (int i = threadIdx.x; i < D; i += kNormThreads) o[i] = static_cast<_Float16>(x[i] * inv * w[i]);
+    for (int i = threadIdx.x; i < D; i += kNormThreads) o[i] = norm_out(x[i], inv, w[i]);
   }
+}
+
+// One token's norm and the dense (f16b) router product in one launch, for the mixture of
+// experts at decode (src/engine.mm:965-991: encode_rms, then the router linear): workgroup
+// b takes router tile b, forms the normed row itself (threads 0..255 sum the squares in
+// rms_norm_kernel's order, waves 0..3 meet as norm_total meets them, every element is
+// norm_out's), keeps it in LDS, and multiplies it into its tile as dense_f16_kernel does
+// (the waves split the K steps into ranges of spw, chain their MFMAs, add their partials in
+// wave order), so logits and normed row have the bits of rl_norm followed by rl_linear.
+// Workgroup 0 also writes the normed row for the expert kernels. Waves: dense_f16_kernel's
+// for this K (at least 4, for the norm's 256 threads); spw <= 8 (one batch of loads).
+constexpr int kDenseStep = 32;   // inputs per 1 KB block of the dense f16 layout (dense.hip)
+
+template <int PER>
+__global__ __launch_bounds__(1024) void norm_router_kernel(const float *h, const float *nw, int D, float eps,
+                                                           _Float16 *xn_out, const u32x4 *w, int N, int spw,
+                                                           float *y) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  float *part = reinterpret_cast<float *>(lds);                                   // [4]
+  _Float16 *xs = reinterpret_cast<_Float16 *>(lds + 16);                          // [D]
+  f32x4 *red = reinterpret_cast<f32x4 *>(lds + 16 + ((size_t)D * 2 + 15) / 16 * 16);   // [waves-1][64]
+  const int waves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, j4 = lane >> 4;
+  const int t = blockIdx.x;
+  const int steps = D / kDenseStep;
+  const int s0 = wave * spw, s1 = min(steps, s0 + spw);
+  // the norm's loads first (threads 0..255, rms_norm_kernel<PER>'s elements), then the
+  // router tile's: the first wait is for the norm's only
+  const bool nt = threadIdx.x < kNormThreads;
+  const __amdgpu_buffer_rsrc_t rh = make_rsrc(h, nt ? (uint32_t)D * 4u : 0u), rn = make_rsrc(nw, nt ? (uint32_t)D * 4u : 0u);
+  float xv[PER], wv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    xv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                          rh, 4u * (threadIdx.x + (uint32_t)j * kNormThreads), 0, 0));
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    wv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                          rn, 4u * (threadIdx.x + (uint32_t)j * kNormThreads), 0, 0));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((size_t)t * steps + s0) * 64, (uint32_t)max(0, s1 - s0) * 1024u);
+  u32x4 wb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    wb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, 16u * lane + (uint32_t)i * 1024u, 0,
+                                                                           kNonTemporal));
+  __builtin_amdgcn_sched_barrier(0);
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) ss = __builtin_fmaf(xv[j], xv[j], ss);
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) ss += __shfl_xor(ss, d);
+  if (nt && lane == 0) part[wave] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int wv4 = 0; wv4 < kNormThreads / 64; ++wv4) total += part[wv4];
+  const float inv = 1.0f / __builtin_sqrtf(total / (float)D + eps);
+  if (nt) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = threadIdx.x + j * kNormThreads;
+      if (i < D) {
+        const _Float16 v = norm_out(xv[j], inv, wv[j]);
+        xs[i] = v;
+        if (t == 0) xn_out[i] = v;
+      }
+    }
+  }
+  __syncthreads();
+  // dense_f16_kernel's products for token row 0 (lanes c16 = 0; the other rows are zeros)
+  f32x4 acc = {};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int st = s0 + i;
+    const u32x4 xb = c16 == 0 && st < s1 ? *reinterpret_cast<const u32x4 *>(xs + st * kDenseStep + 8 * j4)
+                                         : u32x4{0u, 0u, 0u, 0u};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xb), __builtin_bit_cast(half8, wb[i]), acc,
+                                                 0, 0, 0);
+  }
+  acc = reduce_waves(acc, red, wave, waves, lane);
+  const int n = 16 * t + c16;
+  if (wave == 0 && j4 == 0 && n < N) y[n] = acc[0];
 }
 
 // Top-k with rl_top_k's order (value descending, equal values by index ascending, NaN left
@@ -527,21 +615,26 @@ static int norm_with(rl_engine *e, const float *w, const float *h, int h_stride,
   return 0;
 }
 
+// the weight of norm `which` (0 input, 1 post-attention, 2 final) of a layer: native files'
+// folded copies, the file's own float tensor otherwise; nullptr when the file has none
+static const float *norm_weight(rl_engine *e, int which, int layer) {
+  const ModelConfig &c = e->model->config();
+  if (c.native) {
+    const DevMem &m = which == 2 ? e->norm_final : which == 0 ? e->norm_in[layer] : e->norm_post[layer];
+    return m.as<float>();
+  }
+  const std::string name = which == 2 ? std::string("final_norm") : lname(layer, which == 0 ? "in_norm" : "post_norm");
+  auto it = e->floats.find(name);
+  return it == e->floats.end() ? nullptr : it->second.as<float>();
+}
+
 static int norm_rows(rl_engine *e, int which, int layer, const float *h, int h_stride, int rows, _Float16 *xn,
                      int xn_stride, hipStream_t st) {
   const ModelConfig &c = e->model->config();
   RLQ_REQUIRE(which >= 0 && which <= 2, "rl_norm: which=%d (0 input, 1 post-attention, 2 final)", which);
   RLQ_REQUIRE(which == 2 || (layer >= 0 && layer < c.layers), "rl_norm: layer %d of %d", layer, c.layers);
   RLQ_REQUIRE(h && xn && rows >= 1 && h_stride >= c.hidden && xn_stride >= c.hidden, "rl_norm: bad rows or strides");
-  const float *w = nullptr;
-  if (c.native) {
-    const DevMem &m = which == 2 ? e->norm_final : which == 0 ? e->norm_in[layer] : e->norm_post[layer];
-    w = m.as<float>();
-  } else {
-    const std::string name = which == 2 ? std::string("final_norm") : lname(layer, which == 0 ? "in_norm" : "post_norm");
-    auto it = e->floats.find(name);
-    w = it == e->floats.end() ? nullptr : it->second.as<float>();
-  }
+  const float *w = norm_weight(e, which, layer);
   RLQ_REQUIRE(w, "model has no float tensor for norm %d of layer %d", which, layer);
   return norm_with(e, w, h, h_stride, rows, xn, xn_stride, st);
 }
@@ -586,6 +679,64 @@ static int top_k_device(rl_engine *e, const float *x, int n, int k, int32_t *ids
     vals[r] = v[r];
   }
   return got;
+}
+
+// One token of a mixture of experts: post-attention norm and router product in one launch
+// (norm_router_kernel), the normed row left in e->xn and the logits in e->router_logits, as
+// rl_norm and rl_linear leave them. Returns 1 (nothing launched) when the router is not a
+// dense f16b matrix or its shape is outside the kernel's (fewer than 4 waves, more than 8
+// K steps per wave, rows past the norm's register form).
+static int norm_router_one_token(rl_engine *e, int layer, const float *h, hipStream_t st) {
+  const ModelConfig &c = e->model->config();
+  const EngineTensor *router = tensor_of(e, lname(layer, "moe.router"));
+  const float *w = norm_weight(e, 1, layer);
+  if (!router || !w || router->q->kind != kKindF16b || router->q->k != c.hidden || c.hidden % kDenseStep) return 1;
+  const int H = c.hidden, steps = H / kDenseStep;
+  // dense_f16_kernel's split of the K steps over the waves (rlq_linear_f16)
+  const int waves = std::min(16, (steps + 7) / 8);
+  const int spw = ((steps + waves - 1) / waves + 7) / 8 * 8;
+  const int per = (H + kNormThreads - 1) / kNormThreads;
+  if (waves < kNormThreads / 64 || spw > 8 || per > kNormMaxPer) return 1;
+  RLQ_REQUIRE(router->q->n >= c.experts + 1 && router->q->n_pad == e->router_stride,
+              "layer %d: router is %d x %d, needs %d x %d", layer, router->q->n, router->q->k, c.experts + 1, H);
+  const size_t lds = 16 + ((size_t)H * 2 + 15) / 16 * 16 + (size_t)(waves - 1) * 64 * 16;
+  auto launch = [&](auto kernel) {
+    kernel<<<tiles_of(router->q->n), 64 * waves, lds, st>>>(h, w, H, c.norm_eps, e->xn.as<_Float16>(),
+                                                            router->packed.as<u32x4>(), router->q->n, spw,
+                                                            e->router_logits.as<float>());
+  };
+  if (per <= 8) launch(norm_router_kernel<8>);
+  else if (per <= 16) launch(norm_router_kernel<16>);
+  else if (per <= 20) launch(norm_router_kernel<20>);
+  else launch(norm_router_kernel<kNormMaxPer>);
+  RLQ_HIP(hipGetLastError());
+  return 0;
+}
+
+// The experts of a mixture-of-experts layer once the normed rows (e->xn) and the router
+// logits are in place: routing, gate/up, SwiGLU, down and the combine into h.
+static int moe_experts(rl_engine *e, int layer, float *h, int h_stride, int T, hipStream_t st) {
+  const ModelConfig &c = e->model->config();
+  _Float16 *xn = e->xn.as<_Float16>();
+  const EngineTensor *router = tensor_of(e, lname(layer, "moe.router"));
+  const EngineTensor *gu = tensor_of(e, lname(layer, "moe.gate_up"));
+  const EngineTensor *dn = tensor_of(e, lname(layer, "moe.down"));
+  RLQ_REQUIRE(router && gu && dn, "layer %d: the mixture of experts needs moe.router, moe.gate_up and moe.down", layer);
+  const int E = c.experts, E1 = E + 1, H = c.hidden, I = c.moe_inter;
+  RLQ_REQUIRE(router->q->n >= E1 && router->q->k == H && router->q->n_pad == e->router_stride,
+              "layer %d: router is %d x %d, needs %d x %d", layer, router->q->n, router->q->k, E1, H);
+  RLQ_REQUIRE(gu->q->n == E1 * 2 * I && gu->q->k == H && dn->q->n == E1 * H && dn->q->k == I,
+              "layer %d: expert stacks do not match %d experts of %d x %d", layer, E1, I, H);
+  RLQ_REQUIRE(gu->q->native == dn->q->native, "layer %d: gate/up and down stacks of different formats", layer);
+  const float *logits = e->router_logits.as<float>();
+  if (!gu->q->native)
+    return rlq_moe(xn, e->x_stride, logits, e->router_stride, T, E, c.experts_per_tok, c.norm_topk ? 1 : 0, H, I,
+                   gu->packed.p, dn->packed.p, RLQ_BF16, h, h_stride, e->moe_ws.p, e->moe_ws.bytes, st);
+  const std::string &bk = gu->q->book.empty() ? c.book : gu->q->book;
+  return rlq_moe_native(xn, e->x_stride, logits, e->router_stride, T, E, c.experts_per_tok, c.norm_topk ? 1 : 0, H, I,
+                        gu->packed.p, gu->srow.as<float>(), dn->packed.p, dn->srow.as<float>(), e->slots.as<int>(), E1,
+                        bk == "fp4" ? RLQ_BOOK_FP4 : RLQ_BOOK_INT15, dn->col.as<float>(), h, h_stride, e->moe_ws.p,
+                        e->moe_ws.bytes, st);
 }
 
 }  // namespace rlq
@@ -638,6 +789,13 @@ int rl_mlp(rl_engine *e, int layer, float *h, int h_stride, int T, void *stream)
               e->max_chunk);
   auto st = static_cast<hipStream_t>(stream);
   _Float16 *xn = e->xn.as<_Float16>();
+  if (c.is_moe() && T == 1) {
+    // one token of a mixture of experts: the norm and the router product in one launch
+    // (norm_router_kernel: the bits of the two steps)
+    const int fused = norm_router_one_token(e, layer, h, st);
+    if (fused < 0) return fused;
+    if (fused == 0) return moe_experts(e, layer, h, h_stride, T, st);
+  }
   if (int rc = norm_rows(e, 1, layer, h, h_stride, T, xn, e->x_stride, st)) return rc;
   if (!c.is_moe()) {
     // encode_mlp (src/engine.mm:943-958): gate_up, SwiGLU with down's column scale, down + h
@@ -671,25 +829,13 @@ int rl_mlp(rl_engine *e, int layer, float *h, int h_stride, int T, void *stream)
   }
   // encode_moe (src/engine.mm:965-1059)
   const EngineTensor *router = tensor_of(e, lname(layer, "moe.router"));
-  const EngineTensor *gu = tensor_of(e, lname(layer, "moe.gate_up"));
-  const EngineTensor *dn = tensor_of(e, lname(layer, "moe.down"));
-  RLQ_REQUIRE(router && gu && dn, "layer %d: the mixture of experts needs moe.router, moe.gate_up and moe.down", layer);
-  const int E = c.experts, E1 = E + 1, H = c.hidden, I = c.moe_inter;
-  RLQ_REQUIRE(router->q->n >= E1 && router->q->k == H && router->q->n_pad == e->router_stride,
-              "layer %d: router is %d x %d, needs %d x %d", layer, router->q->n, router->q->k, E1, H);
-  RLQ_REQUIRE(gu->q->n == E1 * 2 * I && gu->q->k == H && dn->q->n == E1 * H && dn->q->k == I,
-              "layer %d: expert stacks do not match %d experts of %d x %d", layer, E1, I, H);
-  RLQ_REQUIRE(gu->q->native == dn->q->native, "layer %d: gate/up and down stacks of different formats", layer);
+  RLQ_REQUIRE(router, "layer %d: the mixture of experts needs moe.router", layer);
+  RLQ_REQUIRE(router->q->n >= c.experts + 1 && router->q->k == c.hidden && router->q->n_pad == e->router_stride,
+              "layer %d: router is %d x %d, needs %d x %d", layer, router->q->n, router->q->k, c.experts + 1,
+              c.hidden);
   float *logits = e->router_logits.as<float>();
   if (int rc = linear_rows(e, *router, 0, router->q->n, xn, e->x_stride, T, logits, e->router_stride, 0, st)) return rc;
-  if (!gu->q->native)
-    return rlq_moe(xn, e->x_stride, logits, e->router_stride, T, E, c.experts_per_tok, c.norm_topk ? 1 : 0, H, I,
-                   gu->packed.p, dn->packed.p, RLQ_BF16, h, h_stride, e->moe_ws.p, e->moe_ws.bytes, st);
-  const std::string &bk = gu->q->book.empty() ? c.book : gu->q->book;
-  return rlq_moe_native(xn, e->x_stride, logits, e->router_stride, T, E, c.experts_per_tok, c.norm_topk ? 1 : 0, H, I,
-                        gu->packed.p, gu->srow.as<float>(), dn->packed.p, dn->srow.as<float>(), e->slots.as<int>(), E1,
-                        bk == "fp4" ? RLQ_BOOK_FP4 : RLQ_BOOK_INT15, dn->col.as<float>(), h, h_stride, e->moe_ws.p,
-                        e->moe_ws.bytes, st);
+  return moe_experts(e, layer, h, h_stride, T, st);
 }
 
 const float *rl_head(rl_engine *e, const float *h, int h_stride, int rows, void *stream) {

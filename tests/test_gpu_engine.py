@@ -211,6 +211,30 @@ def test_moe_mlp(gpu, tmp_path, book):
         assert hits.value == 0 and loads.value == 0
 
 
+@pytest.mark.parametrize("book", [None, "int15"])
+@pytest.mark.parametrize("hidden", [1024, 2048])
+def test_moe_mlp_one_token_norm_and_router_in_one_launch(gpu, tmp_path, book, hidden):
+    """At one token of a MoE layer whose router K takes 4 waves or more, rl_mlp runs the
+    post-attention norm and the router product in one launch: the token's result is within
+    the bar of the oracle and bit-identical to the same token inside a 3-token call (the
+    norm and the router as separate launches; the experts read the normed row the fused
+    launch leaves, so equal bits also pin that row)."""
+    import torch
+
+    m = MF.write_moe_model(str(tmp_path / "moe.rlm"), seed=hidden + 3, native_book=book, hidden=hidden, experts=32,
+                           topk=4, moe_inter=256)
+    with Engine(m.path, max_chunk=16) as e:
+        h0 = np.random.default_rng(hidden).standard_normal((3, hidden)).astype(np.float32)
+        h3 = to_dev(h0, gpu)
+        e.mlp(0, h3)
+        h1 = to_dev(h0[1:2].copy(), gpu)
+        e.mlp(0, h1)
+        _sync()
+        assert torch.equal(h1[0], h3[1])
+        ref = _moe_ref(m, 0, h0[1:2])
+        O.check_close(h1.cpu().numpy().astype(np.float64) - h0[1:2], ref - h0[1:2], TOL, f"MoE T=1 H={hidden}")
+
+
 def _check_layer(got, ref, what):
     """A layer's contribution through fp16 activations, against the fp64 reference that
     rounds the same activations: where the kernel's fp32 value and the fp64 one fall on

@@ -138,7 +138,7 @@ int rl_top_k_device(rl_engine *e, const float *logits, int n, int k, int32_t *id
 
 /* src/capi.h:39: the index of the largest of the first rl_vocab() logits of row 0 of the last
  * rl_head call (the lowest index among equal ones). Runs on the stream that rl_head call ran
- * on, and waits for it. */
+ * on (which must still exist), and waits for it. */
 int rl_argmax(const rl_engine *e);
 
 #ifdef __cplusplus
